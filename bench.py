@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Benchmark: SSA attention forward + backward on one MI355X.
+
+A "step" is one forward + backward of the SSA attention op through the
+reference-compatible kernel API (ssa_flash_attn_forward +
+ssa_flash_attn_backward) on synthetic inputs already resident in HBM:
+B=4, H=16, S=4096, D=128, bf16, causal, Q/K/V = 0.5 N(0,1), dO ~ N(0,1),
+n=1.5, b=0.8, scale=1/sqrt(D) (the shape BASELINE.json's metric is quoted on).
+
+value = algorithmic fwd+bwd FLOPs / step time, with fwd = 4 D pairs and
+bwd = 10 D pairs (pairs = unmasked (q, k) pairs), i.e. 14 D pairs per step.
+
+Also reported on the same JSON line:
+  roofline     -- the dominant kernel's algorithmic FLOPs (or bytes) per launch
+                  over its average launch time, measured here with HIP events
+                  on the stream the kernel runs on;
+  kernels      -- the same for every kernel of the step;
+  cpu_baseline -- the PyTorch-eager fp32 oracle (oracle/ssa_oracle_torch.py)
+                  on the host cores, on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import re
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "luciole-1b_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+# MI355X published dense peaks.
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (2.5 PFLOP/s class)
+PEAK_HBM_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (B, Hq, Hkv, S, D, causal)
+    "s4096": (4, 16, 16, 4096, 128, True),   # north star: BASELINE.json metric shape
+    "s2048": (4, 16, 16, 2048, 128, True),
+    "s16384": (1, 16, 16, 16384, 128, True),
+    "gqa_d64": (4, 32, 8, 4096, 64, True),   # production Luciole-1B attention shape
+}
+
+METRIC = "SSA attn fwd+bwd TFLOP/s and % bf16 MFMA peak, 1 MI355X, S=4096 D=128"
+
+
+def pairs_dense(B, Hq, S, causal):
+    return B * Hq * (S * (S + 1) // 2 if causal else S * S)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        m = re.search(r"Model name:\s*(.+)", out)
+        if m:
+            return m.group(1).strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(S, D, causal, budget_s=20.0):
+    """Time the fp32 PyTorch-eager oracle on (b, h) slices of the workload on the host."""
+    import torch
+
+    from oracle.ssa_oracle_torch import run_reference_grads
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(1234)
+    q = torch.randn(1, 1, S, D, generator=g) * 0.5
+    k = torch.randn(1, 1, S, D, generator=g) * 0.5
+    v = torch.randn(1, 1, S, D, generator=g) * 0.5
+    do = torch.randn(1, 1, S, D, generator=g)
+    n = torch.tensor(1.5)
+    b = torch.tensor(0.8)
+    scale = 1.0 / math.sqrt(D)
+    run_reference_grads(q, k, v, scale, n, b, do, causal)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        run_reference_grads(q, k, v, scale, n, b, do, causal)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = 14 * D * pairs_dense(1, 1, S, causal)
+    return {
+        "value": flops / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} runs of one (b,h) slice S={S} D={D} fp32 causal={int(causal)} "
+                   f"fwd+autograd bwd, median {med * 1e3:.1f} ms; os.cpu_count()={threads}; "
+                   f"cpu={cpu_model()}"),
+        "ms_per_slice": med * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="s4096", choices=sorted(CONFIGS))
+    ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the SSA op has no cross-GPU "
+                                   "communication (see DESIGN.md, sharding); run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+
+    from SSA.ssa_hip_kernel import BackwardLaunch, ssa_flash_attn_backward, ssa_flash_attn_forward
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    torch.manual_seed(1234)
+    q = (torch.randn(B, Hq, S, D, device=dev) * 0.5).to(dtype)
+    k = (torch.randn(B, Hkv, S, D, device=dev) * 0.5).to(dtype)
+    v = (torch.randn(B, Hkv, S, D, device=dev) * 0.5).to(dtype)
+    do = torch.randn(B, Hq, S, D, device=dev).to(dtype)
+    n = torch.tensor(1.5, device=dev)
+    bb = torch.tensor(0.8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    pairs = pairs_dense(B, Hq, S, causal)
+    flops_fwd = 4 * D * pairs
+    flops_bwd = 10 * D * pairs
+
+    def step():
+        out, m = ssa_flash_attn_forward(q, k, v, scale, n, bb, causal)
+        return ssa_flash_attn_backward(q, k, v, out, do, m, scale, n, bb, causal)
+
+    log(f"[bench] config={args.config} B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal} warmup={args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed / args.steps * 1e3
+    value = (flops_fwd + flops_bwd) / (ms_step * 1e-3) / 1e12
+
+    # Per-kernel launch durations, HIP events on the stream the kernels use.
+    log("[bench] per-kernel timing")
+    stream = torch.cuda.current_stream(dev)
+    out, m = ssa_flash_attn_forward(q, k, v, scale, n, bb, causal)
+    launch = BackwardLaunch(q, k, v, out, do, m, scale, n, bb, causal)
+
+    def time_launch(fn, iters):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+        for a, e in evs:
+            a.record(stream)
+            fn()
+            e.record(stream)
+        torch.cuda.synchronize()
+        ts = sorted(a.elapsed_time(e) for a, e in evs)
+        return sum(ts) / len(ts), ts[len(ts) // 2]
+
+    it = args.kernel_iters
+    kernels = {}
+    avg, med = time_launch(lambda: ssa_flash_attn_forward(q, k, v, scale, n, bb, causal), it)
+    kernels["ssa_fwd_kernel"] = {"avg_ms": avg, "median_ms": med, "alg_flop": flops_fwd}
+    for stage in BackwardLaunch.STAGES:
+        avg, med = time_launch(lambda s=stage: launch.run_stage(s), it)
+        kernels[f"ssa_bwd_{stage}_kernel"] = {"avg_ms": avg, "median_ms": med}
+    # Algorithmic work per launch: dK/dV does QK^T, dP, dV, dK (8 D per pair);
+    # dQ adds only its dQ product (2 D per pair); preprocess moves O, dO, Delta.
+    kernels["ssa_bwd_dkdv_kernel"]["alg_flop"] = 8 * D * pairs
+    kernels["ssa_bwd_dq_kernel"]["alg_flop"] = 2 * D * pairs
+    esize = 2
+    pre_bytes = 2 * B * Hq * S * D * esize + 4 * B * Hq * S
+    kernels["ssa_bwd_preprocess_kernel"]["alg_bytes"] = pre_bytes
+    for name, kd in kernels.items():
+        if "alg_flop" in kd:
+            kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
+            kd["frac_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
+        if "alg_bytes" in kd:
+            kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
+            kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
+    dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
+    kd = kernels[dominant]
+    if "tflops" in kd:
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": kd["tflops"] / PEAK_BF16_TFLOPS, "traffic": None,
+                    "avg_launch_ms": kd["avg_ms"]}
+    else:
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": kd["gbps"], "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": None,
+                    "avg_launch_ms": kd["avg_ms"]}
+
+    fwd_ms = kernels["ssa_fwd_kernel"]["avg_ms"]
+    bwd_ms = sum(kernels[f"ssa_bwd_{s}_kernel"]["avg_ms"] for s in BackwardLaunch.STAGES)
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: Q/K/V = 0.5 N(0,1), dO ~ N(0,1), seed 1234, n=1.5, b=0.8",
+        "config": {"workload": f"SSA attention fwd+bwd ({args.config})", "B": B, "Hq": Hq, "Hkv": Hkv,
+                   "S": S, "D": D, "causal": causal, "pairs": pairs,
+                   "alg_gflop_per_step": (flops_fwd + flops_bwd) / 1e9},
+        "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
+        "fwd_tflops": flops_fwd / (fwd_ms * 1e-3) / 1e12,
+        "bwd_tflops": flops_bwd / (bwd_ms * 1e-3) / 1e12,
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": None,
+        "device": torch.cuda.get_device_name(0),
+        "cu_count": torch.cuda.get_device_properties(0).multi_processor_count,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(S, D, causal)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

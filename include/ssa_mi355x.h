@@ -1,0 +1,148 @@
+/*
+ * ssa_mi355x.h -- C ABI of the MI355X (gfx950) SSA flash-attention library
+ * (libssa_mi355x.so).
+ *
+ * SSA = softmax-substituted attention: logits s = scale * q.k are replaced by
+ * t(s) = n * sign(s) * ln(1 + b |s|) before a row softmax.  This library is the
+ * device half of the drop-in replacement for the reference's Triton launch
+ * layer; the Python host side (luciole-1b_amd/SSA) binds these entry points
+ * with ctypes.
+ *
+ * Conventions
+ *  - Every entry point validates its arguments on the host and returns a
+ *    status (SSA_OK = 0) before any launch; nothing is launched on error.
+ *  - The library never allocates or frees device memory.  Outputs and
+ *    workspaces are passed in by the caller.
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ *    default stream).  No entry point synchronises the device or reads device
+ *    memory on the host (n and b are read by the kernels through pointers).
+ *  - Tensors are [batch, heads, seqlen, head_dim] views described by a base
+ *    pointer and element strides for the first three dimensions; the last
+ *    (head_dim) stride must be 1.  Base pointers must be 16-byte aligned and
+ *    the three strides multiples of 8 elements.
+ *  - Results are bitwise deterministic run to run: no floating-point atomics,
+ *    fixed-order reductions only.
+ */
+#ifndef SSA_MI355X_H
+#define SSA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSA_ABI_VERSION 1
+
+/* Status codes. */
+enum {
+  SSA_OK = 0,
+  SSA_ERR_NULL_POINTER = 1,   /* a required pointer is NULL                       */
+  SSA_ERR_SHAPE = 2,          /* bad batch/heads/seqlen (e.g. Hq % Hkv != 0)      */
+  SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128                  */
+  SSA_ERR_DTYPE = 4,          /* dtype not SSA_DTYPE_BF16 / SSA_DTYPE_FP16        */
+  SSA_ERR_ALIGNMENT = 5,      /* base pointer or stride not 16-byte aligned       */
+  SSA_ERR_LAUNCH = 6,         /* the HIP runtime rejected a kernel launch         */
+  SSA_ERR_CU_SEQLENS = 7      /* varlen: bad document table                       */
+};
+
+/* Element types of q/k/v/out/dout/dq/dk/dv. */
+enum { SSA_DTYPE_BF16 = 0, SSA_DTYPE_FP16 = 1 };
+
+/* A [B, H, S, D] tensor view; strides in elements, stride(D) == 1. */
+typedef struct ssa_tensor4 {
+  void* ptr;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_s;
+} ssa_tensor4;
+
+typedef struct ssa_fwd_args {
+  ssa_tensor4 q;        /* [B, Hq,  N, D] */
+  ssa_tensor4 k;        /* [B, Hkv, N, D] */
+  ssa_tensor4 v;        /* [B, Hkv, N, D] */
+  ssa_tensor4 out;      /* [B, Hq,  N, D], written */
+  float* m;             /* [B, Hq, N] contiguous fp32, written: log2(sum_j exp(t_ij)) */
+  const float* ssa_n;   /* device fp32 scalar n */
+  const float* ssa_b;   /* device fp32 scalar b */
+  int32_t batch, heads_q, heads_kv, seqlen, head_dim;
+  int32_t dtype;        /* SSA_DTYPE_* */
+  int32_t causal;       /* 0 / 1: top-left aligned causal mask */
+  float softmax_scale;
+} ssa_fwd_args;
+
+typedef struct ssa_bwd_args {
+  ssa_tensor4 q, k, v;  /* as in ssa_fwd_args */
+  ssa_tensor4 out;      /* forward output */
+  ssa_tensor4 dout;     /* incoming gradient, [B, Hq, N, D] */
+  ssa_tensor4 dq;       /* written, [B, Hq,  N, D] */
+  ssa_tensor4 dk;       /* written, [B, Hkv, N, D] */
+  ssa_tensor4 dv;       /* written, [B, Hkv, N, D] */
+  const float* m;       /* [B, Hq, N] fp32 from ssa_fwd */
+  float* delta;         /* workspace [B, Hq, N] fp32: rowsum(dout * out) */
+  float* partials;      /* workspace, ssa_bwd_partials_count() fp32 */
+  float* dn;            /* device fp32 scalar, written: dL/dn */
+  float* db;            /* device fp32 scalar, written: dL/db */
+  const float* ssa_n;
+  const float* ssa_b;
+  int32_t batch, heads_q, heads_kv, seqlen, head_dim;
+  int32_t dtype;
+  int32_t causal;
+  float softmax_scale;
+} ssa_bwd_args;
+
+/* Library ABI version (SSA_ABI_VERSION). */
+int32_t ssa_abi_version(void);
+
+/* Human-readable text of a status code (static storage). */
+const char* ssa_status_string(int32_t status);
+
+/* Number of fp32 elements the `partials` workspace of ssa_bwd needs. */
+int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen);
+
+/*
+ * Forward: out = softmax_rows(t(scale q k^T) [masked]) v, plus the base-2 row
+ * normaliser m.  Replaces ssa_flash_attn_forward / _ssa_attn_fwd of
+ * training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:732-792 (launch) and
+ * :40-260 (kernel).
+ */
+int32_t ssa_fwd(const ssa_fwd_args* args, void* stream);
+
+/*
+ * Backward: delta = rowsum(dout * out), then dk/dv (+ dn/db partials) and dq
+ * with recompute from m, then a fixed-order reduction of the partials into
+ * dn and db.  Replaces ssa_flash_attn_backward of ssa_triton_kernel.py:795-897
+ * (kernels :267-298, :305-481, :488-719 and the two torch .sum() calls at
+ * :894-895).
+ */
+int32_t ssa_bwd(const ssa_bwd_args* args, void* stream);
+
+/*
+ * Only the first step of ssa_bwd: delta = rowsum(dout * out) in fp32.
+ * Replaces _ssa_attn_bwd_preprocess (ssa_triton_kernel.py:267-298, launched at
+ * :827-840).  Reads args->out, args->dout, writes args->delta; other fields
+ * unused except the shape/dtype fields.
+ */
+int32_t ssa_bwd_preprocess(const ssa_bwd_args* args, void* stream);
+
+/*
+ * The individual steps of ssa_bwd, for callers that schedule or time them
+ * separately.  Each takes the full ssa_bwd_args and must run in this order on
+ * one stream: preprocess, dkdv, dq, reduce.
+ *  - ssa_bwd_dkdv: dk, dv and the dn/db partials (reads delta).  Replaces
+ *    Part 1 of _ssa_attn_bwd + _ssa_attn_bwd_dkdv (ssa_triton_kernel.py:305-401,
+ *    545-636).
+ *  - ssa_bwd_dq: dq (reads delta).  Replaces Part 2 of _ssa_attn_bwd +
+ *    _ssa_attn_bwd_dq (ssa_triton_kernel.py:408-481, 638-719).
+ *  - ssa_bwd_reduce: dn, db from the partials in a fixed order.  Replaces
+ *    dn_partial.sum() / db_partial.sum() (ssa_triton_kernel.py:894-895).
+ */
+int32_t ssa_bwd_dkdv(const ssa_bwd_args* args, void* stream);
+int32_t ssa_bwd_dq(const ssa_bwd_args* args, void* stream);
+int32_t ssa_bwd_reduce(const ssa_bwd_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSA_MI355X_H */

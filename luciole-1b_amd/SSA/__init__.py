@@ -1,0 +1,15 @@
+"""SSA (softmax-substituted attention) for MI355X: hand-written gfx950 HIP
+kernels behind the reference's Python operator interface.
+
+Modules mirror the reference package ``training/train/train_ssa_triton/SSA``:
+``ssa_flash_attention`` (autograd boundary), ``ssa_triton_kernel`` (launch
+layer names, re-exported from ``ssa_hip_kernel``).
+"""
+
+from .ssa_flash_attention import SSAFlashAttnFunc, ssa_flash_attention  # noqa: F401
+from .ssa_hip_kernel import (  # noqa: F401
+    ssa_bwd_preprocess,
+    ssa_flash_attn_backward,
+    ssa_flash_attn_forward,
+    warmup_ssa_triton_kernels,
+)

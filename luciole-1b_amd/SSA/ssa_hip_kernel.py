@@ -1,0 +1,209 @@
+"""Kernel-level SSA attention API on MI355X (gfx950 HIP kernels via a C ABI).
+
+Same functions, argument meaning and return values as the reference launch
+layer ``training/train/train_ssa_triton/SSA/ssa_triton_kernel.py``:
+
+* ``ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True) -> (out, m)``
+  (reference :732-792)
+* ``ssa_flash_attn_backward(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True)
+  -> (dq, dk, dv, dn, db)`` (reference :795-897)
+* ``warmup_ssa_triton_kernels(B, Hq, Hkv, N, D, dtype, device)`` (reference :904-928)
+
+Tensors are ``[B, H, N, D]`` with any strides whose last one is 1 (other
+layouts are made contiguous first); outputs follow the input strides
+(``torch.empty_like``).  ``m`` is the fp32 base-2 row normaliser
+``log2(sum_j exp(t_ij))``.  ``ssa_n`` / ``ssa_b`` are scalar tensors read on the
+device (no host synchronisation); ``dn`` / ``db`` come back as 0-d fp32 tensors.
+
+Differences from the reference, all widening: any sequence length (the
+reference's backward needs N % 128 == 0), and results are bitwise
+reproducible.  Errors: ``AssertionError`` for ``Hq % Hkv != 0`` and a
+non-power-of-two head dim, as in the reference; ``ValueError`` for head dims
+other than 32/64/128 and dtypes other than bf16/fp16.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.SSA_DTYPE_BF16, torch.float16: _lib.SSA_DTYPE_FP16}
+
+
+def _is_pow2(x: int) -> bool:
+    return x > 0 and (x & (x - 1)) == 0
+
+
+def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` or a contiguous copy so that stride(-1) == 1 and rows are 16-byte aligned."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        return t.contiguous()
+    for dim in range(3):
+        if t.shape[dim] > 1 and t.stride(dim) % 8 != 0:
+            return t.contiguous()
+    return t
+
+
+def _t4(t: torch.Tensor) -> _lib.Tensor4:
+    st = [t.stride(i) if t.shape[i] > 1 else 0 for i in range(3)]
+    return _lib.Tensor4(t.data_ptr(), st[0], st[1], st[2])
+
+
+def _scalar(x, device) -> torch.Tensor:
+    if torch.is_tensor(x):
+        if x.numel() != 1:
+            raise ValueError("ssa_n / ssa_b must be scalar tensors")
+        return x.detach().to(device=device, dtype=torch.float32).reshape(()).contiguous()
+    return torch.tensor(float(x), dtype=torch.float32, device=device)
+
+
+def _check_inputs(q, k, v):
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D [B, H, N, D] tensors")
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    assert Hq % Hkv == 0, f"Hq={Hq} must be divisible by Hkv={Hkv}"
+    assert _is_pow2(D), f"Head dim D={D} must be a power of two"
+    if tuple(k.shape) != (B, Hkv, N, D) or tuple(v.shape) != (B, Hkv, N, D):
+        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {q.dtype}: the MI355X SSA kernels take bf16 or fp16")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share one dtype")
+    if not (q.is_cuda and k.device == q.device and v.device == q.device):
+        raise ValueError("q, k, v must be on the same GPU device")
+    return B, Hq, Hkv, N, D
+
+
+def ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True):
+    """SSA attention forward.  Returns ``(out [B,Hq,N,D], m [B,Hq,N] fp32)``."""
+    B, Hq, Hkv, N, D = _check_inputs(q, k, v)
+    q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
+    n32 = _scalar(ssa_n, q.device)
+    b32 = _scalar(ssa_b, q.device)
+    out = _kernel_layout(torch.empty_like(q))
+    m = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
+    args = _lib.FwdArgs(
+        _t4(q), _t4(k), _t4(v), _t4(out),
+        m.data_ptr(), n32.data_ptr(), b32.data_ptr(),
+        B, Hq, Hkv, N, D, _DTYPES[q.dtype], int(bool(causal)), float(softmax_scale),
+    )
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.check(_lib.lib().ssa_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_fwd")
+    return out, m
+
+
+class BackwardLaunch:
+    """Validated backward arguments plus every buffer they point to.
+
+    ``run()`` enqueues the whole backward (``ssa_bwd``); ``run_stage(name)``
+    enqueues one of ``preprocess``, ``dkdv``, ``dq``, ``reduce`` (in that order)
+    so callers can time or schedule the kernels separately.
+    """
+
+    STAGES = ("preprocess", "dkdv", "dq", "reduce")
+
+    def __init__(self, q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True):
+        B, Hq, Hkv, N, D = _check_inputs(q, k, v)
+        if tuple(out.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape):
+            raise ValueError("out and dout must have the shape of q")
+        if out.dtype != q.dtype:
+            raise ValueError("out must have the dtype of q")
+        self.q, self.k, self.v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
+        self.out = _kernel_layout(out)
+        self.dout = _kernel_layout(dout.to(q.dtype))
+        self.m = m.to(torch.float32).contiguous()
+        if tuple(self.m.shape) != (B, Hq, N):
+            raise ValueError(f"m must be [B, Hq, N] = {(B, Hq, N)}, got {tuple(self.m.shape)}")
+        dev = q.device
+        self.n32 = _scalar(ssa_n, dev)
+        self.b32 = _scalar(ssa_b, dev)
+        self.dq = _kernel_layout(torch.empty_like(self.q))
+        self.dk = _kernel_layout(torch.empty_like(self.k))
+        self.dv = _kernel_layout(torch.empty_like(self.v))
+        self.delta = torch.empty((B, Hq, N), device=dev, dtype=torch.float32)
+        self.lib = _lib.lib()
+        count = int(self.lib.ssa_bwd_partials_count(B, Hkv, N))
+        self.partials = torch.empty(count, device=dev, dtype=torch.float32)
+        self.dn = torch.empty((), device=dev, dtype=torch.float32)
+        self.db = torch.empty((), device=dev, dtype=torch.float32)
+        self.device = dev
+        self.args = _lib.BwdArgs(
+            _t4(self.q), _t4(self.k), _t4(self.v), _t4(self.out), _t4(self.dout),
+            _t4(self.dq), _t4(self.dk), _t4(self.dv),
+            self.m.data_ptr(), self.delta.data_ptr(), self.partials.data_ptr(),
+            self.dn.data_ptr(), self.db.data_ptr(), self.n32.data_ptr(), self.b32.data_ptr(),
+            B, Hq, Hkv, N, D, _DTYPES[q.dtype], int(bool(causal)), float(softmax_scale),
+        )
+
+    def _call(self, fn_name: str) -> None:
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            fn = getattr(self.lib, fn_name)
+            _lib.check(fn(ctypes.byref(self.args), ctypes.c_void_p(stream)), fn_name)
+
+    def run(self) -> None:
+        self._call("ssa_bwd")
+
+    def run_stage(self, name: str) -> None:
+        if name not in self.STAGES:
+            raise ValueError(f"unknown backward stage {name!r}")
+        self._call({"preprocess": "ssa_bwd_preprocess", "dkdv": "ssa_bwd_dkdv",
+                    "dq": "ssa_bwd_dq", "reduce": "ssa_bwd_reduce"}[name])
+
+    def results(self):
+        return self.dq, self.dk, self.dv, self.dn, self.db
+
+
+def ssa_flash_attn_backward(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True):
+    """SSA attention backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors."""
+    launch = BackwardLaunch(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal)
+    launch.run()
+    return launch.results()
+
+
+def ssa_bwd_preprocess(out, dout):
+    """Delta = rowsum(out * dout) in fp32, ``[B, H, N]`` (the backward's first step)."""
+    if out.dim() != 4 or tuple(dout.shape) != tuple(out.shape):
+        raise ValueError("out and dout must be matching [B, H, N, D] tensors")
+    if out.dtype not in _DTYPES or dout.dtype != out.dtype:
+        raise ValueError("out/dout must be bf16 or fp16 with one dtype")
+    B, H, N, D = out.shape
+    out, dout = _kernel_layout(out), _kernel_layout(dout)
+    delta = torch.empty((B, H, N), device=out.device, dtype=torch.float32)
+    args = _lib.BwdArgs()
+    args.out, args.dout = _t4(out), _t4(dout)
+    args.delta = delta.data_ptr()
+    args.batch, args.heads_q, args.heads_kv, args.seqlen, args.head_dim = B, H, H, N, D
+    args.dtype = _DTYPES[out.dtype]
+    with torch.cuda.device(out.device):
+        stream = torch.cuda.current_stream(out.device).cuda_stream
+        _lib.check(_lib.lib().ssa_bwd_preprocess(ctypes.byref(args), ctypes.c_void_p(stream)),
+                   "ssa_bwd_preprocess")
+    return delta
+
+
+def warmup_ssa_triton_kernels(
+    B: int = 2,
+    Hq: int = 24,
+    Hkv: int = 8,
+    N: int = 128,
+    D: int = 32,
+    dtype: torch.dtype = torch.bfloat16,
+    device: str = "cuda",
+):
+    """Run one tiny causal forward + backward (loads the library and its code objects)."""
+    q = torch.randn(B, Hq, N, D, dtype=dtype, device=device)
+    k = torch.randn(B, Hkv, N, D, dtype=dtype, device=device)
+    v = torch.randn(B, Hkv, N, D, dtype=dtype, device=device)
+    ssa_n = torch.tensor(1.5, dtype=torch.float32, device=device)
+    ssa_b = torch.tensor(0.8, dtype=torch.float32, device=device)
+    scale = 1.0 / (D ** 0.5)
+    out, m = ssa_flash_attn_forward(q, k, v, scale, ssa_n, ssa_b, causal=True)
+    dout = torch.randn_like(out)
+    ssa_flash_attn_backward(q, k, v, out, dout, m, scale, ssa_n, ssa_b, causal=True)
+    torch.cuda.synchronize()

@@ -1,0 +1,172 @@
+// C ABI of libssa_mi355x.so: host-side validation and dispatch.
+//
+// Mirrors the checks of the reference launch layer
+// (training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:748-764, 802-809,
+// 852-857) as status codes, plus the layout requirements of these kernels.
+// Nothing is launched unless every check passes.
+#include <stdint.h>
+
+#include "../../include/ssa_mi355x.h"
+#include "ssa_launch.hpp"
+
+namespace {
+
+using ssa::Tensor4;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int32_t check_tensor(const ssa_tensor4& t, bool required) {
+  if (t.ptr == nullptr) return required ? SSA_ERR_NULL_POINTER : SSA_OK;
+  if (!aligned16(t.ptr)) return SSA_ERR_ALIGNMENT;
+  if ((t.stride_b % 8) != 0 || (t.stride_h % 8) != 0 || (t.stride_s % 8) != 0) return SSA_ERR_ALIGNMENT;
+  return SSA_OK;
+}
+
+int32_t check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t N, int32_t D, int32_t dtype) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0) return SSA_ERR_SHAPE;
+  if (Hq % Hkv != 0) return SSA_ERR_SHAPE;
+  // Grid sizes are int32 block counts; keep every product well inside range.
+  if (static_cast<int64_t>(B) * Hq * ((static_cast<int64_t>(N) + 127) / 128) > (1ll << 30)) return SSA_ERR_SHAPE;
+  if (D != 32 && D != 64 && D != 128) return SSA_ERR_HEAD_DIM;
+  if (dtype != SSA_DTYPE_BF16 && dtype != SSA_DTYPE_FP16) return SSA_ERR_DTYPE;
+  return SSA_OK;
+}
+
+Tensor4 to_t4(const ssa_tensor4& t) { return Tensor4{t.ptr, t.stride_b, t.stride_h, t.stride_s}; }
+
+#define SSA_TRY(expr)                 \
+  do {                                \
+    const int32_t st_ = (expr);       \
+    if (st_ != SSA_OK) return st_;    \
+  } while (0)
+
+int32_t fill_bwd(const ssa_bwd_args* a, ssa::BwdParams* p, bool preprocess_only) {
+  if (a == nullptr) return SSA_ERR_NULL_POINTER;
+  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
+  SSA_TRY(check_tensor(a->out, true));
+  SSA_TRY(check_tensor(a->dout, true));
+  if (a->delta == nullptr) return SSA_ERR_NULL_POINTER;
+  if (!preprocess_only) {
+    SSA_TRY(check_tensor(a->q, true));
+    SSA_TRY(check_tensor(a->k, true));
+    SSA_TRY(check_tensor(a->v, true));
+    SSA_TRY(check_tensor(a->dq, true));
+    SSA_TRY(check_tensor(a->dk, true));
+    SSA_TRY(check_tensor(a->dv, true));
+    if (a->m == nullptr || a->partials == nullptr || a->dn == nullptr || a->db == nullptr ||
+        a->ssa_n == nullptr || a->ssa_b == nullptr)
+      return SSA_ERR_NULL_POINTER;
+  }
+  p->q = to_t4(a->q);
+  p->k = to_t4(a->k);
+  p->v = to_t4(a->v);
+  p->o = to_t4(a->out);
+  p->dout = to_t4(a->dout);
+  p->dq = to_t4(a->dq);
+  p->dk = to_t4(a->dk);
+  p->dv = to_t4(a->dv);
+  p->m = a->m;
+  p->delta = a->delta;
+  p->partials = a->partials;
+  p->dn = a->dn;
+  p->db = a->db;
+  p->n_ptr = a->ssa_n;
+  p->b_ptr = a->ssa_b;
+  p->B = a->batch;
+  p->Hq = a->heads_q;
+  p->Hkv = a->heads_kv;
+  p->N = a->seqlen;
+  p->scale = a->softmax_scale;
+  return SSA_OK;
+}
+
+int32_t launch_status(hipError_t e) { return e == hipSuccess ? SSA_OK : SSA_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t ssa_abi_version(void) { return SSA_ABI_VERSION; }
+
+const char* ssa_status_string(int32_t status) {
+  switch (status) {
+    case SSA_OK: return "ok";
+    case SSA_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case SSA_ERR_SHAPE: return "invalid shape (batch/heads/seqlen must be > 0 and Hq % Hkv == 0)";
+    case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128)";
+    case SSA_ERR_DTYPE: return "unsupported dtype (supported: bf16, fp16)";
+    case SSA_ERR_ALIGNMENT: return "tensor base pointer must be 16-byte aligned and strides multiples of 8 elements";
+    case SSA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case SSA_ERR_CU_SEQLENS: return "invalid cu_seqlens";
+    default: return "unknown status";
+  }
+}
+
+int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen) {
+  if (batch <= 0 || heads_kv <= 0 || seqlen <= 0) return 0;
+  return 2ll * batch * heads_kv * ssa::dkdv_key_blocks(seqlen);
+}
+
+int32_t ssa_fwd(const ssa_fwd_args* a, void* stream) {
+  if (a == nullptr) return SSA_ERR_NULL_POINTER;
+  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
+  SSA_TRY(check_tensor(a->q, true));
+  SSA_TRY(check_tensor(a->k, true));
+  SSA_TRY(check_tensor(a->v, true));
+  SSA_TRY(check_tensor(a->out, true));
+  if (a->m == nullptr || a->ssa_n == nullptr || a->ssa_b == nullptr) return SSA_ERR_NULL_POINTER;
+  ssa::FwdParams p;
+  p.q = to_t4(a->q);
+  p.k = to_t4(a->k);
+  p.v = to_t4(a->v);
+  p.o = to_t4(a->out);
+  p.m = a->m;
+  p.n_ptr = a->ssa_n;
+  p.b_ptr = a->ssa_b;
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.N = a->seqlen;
+  p.scale = a->softmax_scale;
+  return launch_status(
+      ssa::launch_fwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
+}
+
+int32_t ssa_bwd_preprocess(const ssa_bwd_args* a, void* stream) {
+  ssa::BwdParams p;
+  SSA_TRY(fill_bwd(a, &p, true));
+  return launch_status(ssa::launch_bwd_preprocess(p, a->dtype, a->head_dim, static_cast<hipStream_t>(stream)));
+}
+
+int32_t ssa_bwd_dkdv(const ssa_bwd_args* a, void* stream) {
+  ssa::BwdParams p;
+  SSA_TRY(fill_bwd(a, &p, false));
+  return launch_status(
+      ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
+}
+
+int32_t ssa_bwd_dq(const ssa_bwd_args* a, void* stream) {
+  ssa::BwdParams p;
+  SSA_TRY(fill_bwd(a, &p, false));
+  return launch_status(
+      ssa::launch_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
+}
+
+int32_t ssa_bwd_reduce(const ssa_bwd_args* a, void* stream) {
+  ssa::BwdParams p;
+  SSA_TRY(fill_bwd(a, &p, false));
+  return launch_status(ssa::launch_reduce_partials(p, static_cast<hipStream_t>(stream)));
+}
+
+int32_t ssa_bwd(const ssa_bwd_args* a, void* stream) {
+  ssa::BwdParams p;
+  SSA_TRY(fill_bwd(a, &p, false));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool causal = a->causal != 0;
+  SSA_TRY(launch_status(ssa::launch_bwd_preprocess(p, a->dtype, a->head_dim, s)));
+  SSA_TRY(launch_status(ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, causal, s)));
+  SSA_TRY(launch_status(ssa::launch_bwd_dq(p, a->dtype, a->head_dim, causal, s)));
+  return launch_status(ssa::launch_reduce_partials(p, s));
+}
+
+}  // extern "C"

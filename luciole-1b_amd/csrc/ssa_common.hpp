@@ -1,0 +1,107 @@
+// Shared device helpers for the gfx950 SSA attention kernels.
+//
+// Matrix-core conventions used by every kernel (v_mfma_f32_32x32x16_{bf16,f16},
+// wave64):
+//   A operand  (32 x 16): lane l holds row (l % 32), 8 k-slots of half (l / 32)
+//   B operand  (16 x 32): lane l holds column (l % 32), the same 8 k-slots
+//   C/D        (32 x 32): lane l holds column (l % 32) and rows
+//                         8*(r/4) + 4*(l/32) + (r%4), r = 0..15
+// The contraction is over k-slots, so any bijection between (half, slot) and
+// the logical k index works as long as A and B use the same one.  The kernels
+// exploit this: an accumulator tile whose 16 rows per lane are
+// {0-3, 8-11, 16-19, 24-27} (+4 for the upper half) feeds the next MFMA as an
+// A or B operand directly, with k-step ks taking accumulator entries 8ks..8ks+7,
+// and the other operand is gathered with the matching row order (crow()).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<__bf16> {
+  typedef bf16x8 type;
+};
+template <>
+struct Vec8<_Float16> {
+  typedef f16x8 type;
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Row (within a 32-row accumulator block) held in accumulator entry r by lane half hh.
+__device__ __forceinline__ int crow(int r, int hh) { return ((r >> 2) << 3) + (hh << 2) + (r & 3); }
+
+template <typename V>
+__device__ __forceinline__ V load16(const void* p) {
+  return __builtin_bit_cast(V, *reinterpret_cast<const u32x4*>(p));
+}
+
+template <typename V>
+__device__ __forceinline__ V zero8() {
+  return __builtin_bit_cast(V, u32x4{0u, 0u, 0u, 0u});
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// Value of `x` in the lane 32 positions away (the other half of the wave).
+__device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs (block id % 8).  This
+// bijection on [0, total) gives each XCD a contiguous range of logical block
+// indices, so logical neighbours (same head) share one XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  const int q = total >> 3, r = total & 7;
+  const int x = bid & 7, j = bid >> 3;
+  return x * q + (x < r ? x : r) + j;
+}
+
+struct Tensor4 {
+  const void* ptr;
+  int64_t sb, sh, ss;
+};
+
+struct FwdParams {
+  Tensor4 q, k, v, o;
+  float* m;
+  const float* n_ptr;
+  const float* b_ptr;
+  int B, Hq, Hkv, N;
+  float scale;
+};
+
+struct BwdParams {
+  Tensor4 q, k, v, o, dout, dq, dk, dv;
+  const float* m;
+  float* delta;
+  float* partials;  // [2][B*Hkv*nkb]: dn terms then db terms
+  float* dn;
+  float* db;
+  const float* n_ptr;
+  const float* b_ptr;
+  int B, Hq, Hkv, N;
+  float scale;
+};
+
+constexpr float kLn2 = 0.69314718055994530942f;
+// Lazy rescaling threshold (log2 units): the running max used for exp2 is only
+// moved when a new row max exceeds it by more than this, so p <= 2^kRescaleTau.
+constexpr float kRescaleTau = 8.0f;
+
+}  // namespace ssa

@@ -1,0 +1,193 @@
+"""CPU oracle for SSA (softmax-substituted) attention, float64 numpy.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker.  The product path (``luciole-1b_amd/SSA``) never imports it and fails
+loudly when the HIP library is missing.
+
+This is a closed-form restatement of the reference's SSA math:
+
+* forward transform ``t = n * sign(s) * log1p(b * |s|)`` with
+  ``s = scale * Q K^T`` -- ``training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:95-107``
+  and the fp32 oracle ``training/train/train_ssa_triton/check_ssa_triton_parity.py:169-206``;
+* softmax over ``t`` per query row, GQA by ``kv_head = q_head // G``
+  (``ssa_triton_kernel.py:192-194``, ``check_ssa_triton_parity.py:183-185``);
+  the softmax is max-subtracted here, where the reference oracle's plain
+  ``w / sum(w)`` (``check_ssa_triton_parity.py:202-204``) overflows for trained
+  values such as n = -302;
+* stored normaliser ``M = log2(sum_j exp(t_j))`` (``ssa_triton_kernel.py:247-255``);
+* backward chain rule ``dT = P (dP - Delta)``, ``dS = dT * n b / (1 + b|s|)``,
+  ``dn = sum dT sign(s) log1p(b|s|)``, ``db = sum dT n sign(s) |s| / (1 + b|s|)``
+  (``ssa_triton_kernel.py:371-397,467-477``), with
+  ``Delta = rowsum(dO * O)`` (``ssa_triton_kernel.py:267-298``).
+
+Varlen (packed sequences, block-diagonal causal over ``cu_seqlens``) has no
+reference implementation (the reference asserts ``packed_seq_params is None``,
+``SSA/ssa_triton_attention.py:154-156``); it is defined here as the
+concatenation of independent dense runs, one per document.
+
+Pinning (tests/test_oracle.py): brute-force pure-Python loops plus central
+finite differences on tiny inputs, torch float64 autograd of an independent
+restatement, n = 0 (cumulative mean), b -> 0 with n b = 1 (softmax attention,
+checked against torch's scaled_dot_product_attention), single-key rows,
+``M`` against scipy's logsumexp, GQA against repeat_interleave, varlen against
+per-document dense runs, causal prefix independence.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+LN2 = math.log(2.0)
+
+
+def _expand_kv(x: np.ndarray, group: int) -> np.ndarray:
+    """[B, Hkv, N, D] -> [B, Hkv*group, N, D], head h reads kv head h // group."""
+    return np.repeat(x, group, axis=1)
+
+
+def _mask(nq: int, nk: int, causal: bool) -> np.ndarray:
+    """Valid (q, k) pairs.  Causal is top-left aligned (key j visible to query i iff j <= i)."""
+    if not causal:
+        return np.ones((nq, nk), dtype=bool)
+    return np.arange(nk)[None, :] <= np.arange(nq)[:, None]
+
+
+def ssa_logits(s: np.ndarray, n: float, b: float) -> np.ndarray:
+    """t(s) = n * sign(s) * log1p(b |s|)  (ssa_triton_kernel.py:98-105)."""
+    return n * np.sign(s) * np.log1p(b * np.abs(s))
+
+
+def ssa_forward(q, k, v, scale, n, b, causal=True):
+    """Dense SSA attention forward in float64.
+
+    q: [B, Hq, N, D]; k, v: [B, Hkv, N, D].  Returns (out [B,Hq,N,D], M [B,Hq,N])
+    where M = log2(sum_j exp(t_ij)) over valid keys (-inf for a row with none).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    bsz, hq, nq, _ = q.shape
+    hkv = k.shape[1]
+    if hq % hkv != 0:
+        raise ValueError(f"Hq={hq} must be divisible by Hkv={hkv}")
+    g = hq // hkv
+    ke, ve = _expand_kv(k, g), _expand_kv(v, g)
+    s = scale * (q @ ke.swapaxes(-1, -2))
+    valid = _mask(nq, k.shape[2], causal)[None, None]
+    t = np.where(valid, ssa_logits(s, n, b), -np.inf)
+    tmax = np.max(t, axis=-1, keepdims=True)
+    tmax_safe = np.where(np.isfinite(tmax), tmax, 0.0)
+    w = np.where(valid, np.exp(t - tmax_safe), 0.0)
+    l = w.sum(axis=-1, keepdims=True)
+    p = np.where(l > 0, w / np.where(l > 0, l, 1.0), 0.0)
+    out = p @ ve
+    with np.errstate(divide="ignore"):
+        m = ((tmax_safe + np.log(l)) / LN2)[..., 0]
+    return out, m
+
+
+def ssa_backward(q, k, v, dout, scale, n, b, causal=True):
+    """Closed-form SSA backward in float64 (loss = sum(out * dout)).
+
+    Returns (dq, dk, dv, dn, db, delta) with delta = rowsum(dout * out).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    do = np.asarray(dout, dtype=np.float64)
+    bsz, hq, nq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    ke, ve = _expand_kv(k, g), _expand_kv(v, g)
+    s = scale * (q @ ke.swapaxes(-1, -2))
+    valid = _mask(nq, k.shape[2], causal)[None, None]
+    s0 = np.where(valid, s, 0.0)
+    lg = np.log1p(b * np.abs(s0))
+    t = np.where(valid, n * np.sign(s0) * lg, -np.inf)
+    tmax = np.max(t, axis=-1, keepdims=True)
+    tmax = np.where(np.isfinite(tmax), tmax, 0.0)
+    w = np.where(valid, np.exp(t - tmax), 0.0)
+    l = w.sum(axis=-1, keepdims=True)
+    p = np.where(l > 0, w / np.where(l > 0, l, 1.0), 0.0)
+    out = p @ ve
+    delta = np.sum(do * out, axis=-1)
+    dp = do @ ve.swapaxes(-1, -2)
+    dt = p * (dp - delta[..., None])
+    ds = dt * (n * b / (1.0 + b * np.abs(s0)))
+    dq = scale * (ds @ ke)
+    dk_e = scale * (ds.swapaxes(-1, -2) @ q)
+    dv_e = p.swapaxes(-1, -2) @ do
+    dk = dk_e.reshape(bsz, hkv, g, *dk_e.shape[2:]).sum(axis=2)
+    dv = dv_e.reshape(bsz, hkv, g, *dv_e.shape[2:]).sum(axis=2)
+    sg = np.sign(s0)
+    dn = float(np.sum(dt * sg * lg))
+    db = float(np.sum(dt * n * sg * np.abs(s0) / (1.0 + b * np.abs(s0))))
+    return dq, dk, dv, dn, db, delta
+
+
+def ssa_forward_backward(q, k, v, dout, scale, n, b, causal=True):
+    """Forward and backward in one call: dict with out, m, dq, dk, dv, dn, db, delta."""
+    out, m = ssa_forward(q, k, v, scale, n, b, causal)
+    dq, dk, dv, dn, db, delta = ssa_backward(q, k, v, dout, scale, n, b, causal)
+    return {"out": out, "m": m, "dq": dq, "dk": dk, "dv": dv, "dn": dn, "db": db, "delta": delta}
+
+
+def ssa_varlen_forward_backward(q, k, v, dout, cu_seqlens, scale, n, b, causal=True):
+    """Packed-sequence SSA: q [T, Hq, D], k/v [T, Hkv, D], cu_seqlens int [ndocs+1].
+
+    Each document [cu[i], cu[i+1]) attends only within itself (block-diagonal,
+    causal inside each block when ``causal``).  Returns a dict like
+    ``ssa_forward_backward`` with token-major tensors ([T, H, D], m/delta [T, H]).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    do = np.asarray(dout, dtype=np.float64)
+    cu = [int(x) for x in np.asarray(cu_seqlens).tolist()]
+    tot, hq, d = q.shape
+    hkv = k.shape[1]
+    res = {
+        "out": np.zeros((tot, hq, d)),
+        "m": np.full((tot, hq), -np.inf),
+        "delta": np.zeros((tot, hq)),
+        "dq": np.zeros((tot, hq, d)),
+        "dk": np.zeros((tot, hkv, d)),
+        "dv": np.zeros((tot, hkv, d)),
+        "dn": 0.0,
+        "db": 0.0,
+    }
+    for i in range(len(cu) - 1):
+        a, e = cu[i], cu[i + 1]
+        if e <= a:
+            continue
+
+        def dense(x):
+            return x[a:e].transpose(1, 0, 2)[None]
+
+        r = ssa_forward_backward(dense(q), dense(k), dense(v), dense(do), scale, n, b, causal)
+        res["out"][a:e] = r["out"][0].transpose(1, 0, 2)
+        res["m"][a:e] = r["m"][0].T
+        res["delta"][a:e] = r["delta"][0].T
+        res["dq"][a:e] = r["dq"][0].transpose(1, 0, 2)
+        res["dk"][a:e] = r["dk"][0].transpose(1, 0, 2)
+        res["dv"][a:e] = r["dv"][0].transpose(1, 0, 2)
+        res["dn"] += r["dn"]
+        res["db"] += r["db"]
+    return res
+
+
+def causal_pairs(bsz: int, hq: int, n: int, causal: bool = True) -> int:
+    """Number of unmasked (q, k) pairs for a dense launch."""
+    return bsz * hq * (n * (n + 1) // 2 if causal else n * n)
+
+
+def varlen_pairs(cu_seqlens, hq: int, causal: bool = True) -> int:
+    cu = [int(x) for x in np.asarray(cu_seqlens).tolist()]
+    tot = 0
+    for i in range(len(cu) - 1):
+        L = cu[i + 1] - cu[i]
+        tot += L * (L + 1) // 2 if causal else L * L
+    return hq * tot
