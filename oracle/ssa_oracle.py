@@ -89,10 +89,14 @@ def ssa_forward(q, k, v, scale, n, b, causal=True):
     return out, m
 
 
-def ssa_backward(q, k, v, dout, scale, n, b, causal=True):
+def ssa_backward(q, k, v, dout, scale, n, b, causal=True, out_for_delta=None):
     """Closed-form SSA backward in float64 (loss = sum(out * dout)).
 
     Returns (dq, dk, dv, dn, db, delta) with delta = rowsum(dout * out).
+    ``out_for_delta``: the forward output the kernel-level backward was given
+    (``ssa_flash_attn_backward(q, k, v, out, dout, m, ...)`` takes it as an
+    input and its preprocess forms delta from it, ssa_triton_kernel.py:291-294);
+    when None, the exact float64 output is used.
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -112,7 +116,7 @@ def ssa_backward(q, k, v, dout, scale, n, b, causal=True):
     w = np.where(valid, np.exp(t - tmax), 0.0)
     l = w.sum(axis=-1, keepdims=True)
     p = np.where(l > 0, w / np.where(l > 0, l, 1.0), 0.0)
-    out = p @ ve
+    out = p @ ve if out_for_delta is None else np.asarray(out_for_delta, dtype=np.float64)
     delta = np.sum(do * out, axis=-1)
     dp = do @ ve.swapaxes(-1, -2)
     dt = p * (dp - delta[..., None])
@@ -128,10 +132,10 @@ def ssa_backward(q, k, v, dout, scale, n, b, causal=True):
     return dq, dk, dv, dn, db, delta
 
 
-def ssa_forward_backward(q, k, v, dout, scale, n, b, causal=True):
+def ssa_forward_backward(q, k, v, dout, scale, n, b, causal=True, out_for_delta=None):
     """Forward and backward in one call: dict with out, m, dq, dk, dv, dn, db, delta."""
     out, m = ssa_forward(q, k, v, scale, n, b, causal)
-    dq, dk, dv, dn, db, delta = ssa_backward(q, k, v, dout, scale, n, b, causal)
+    dq, dk, dv, dn, db, delta = ssa_backward(q, k, v, dout, scale, n, b, causal, out_for_delta)
     return {"out": out, "m": m, "dq": dq, "dk": dk, "dv": dv, "dn": dn, "db": db, "delta": delta}
 
 

@@ -1,11 +1,15 @@
 """Helpers shared by the GPU parity tests: seeded inputs and error statistics.
 
-Error metric (same as the reference harness,
-training/train/train_ssa_triton/check_ssa_triton_parity.py:124-149,206,219-237):
-kernel tensors are compared with the fp64 oracle rounded to the kernel's
-dtype (the reference's oracle returns out.to(q.dtype) and grads in the dtype
-of the leaves).  Pass bar: max |err| <= MAX_ABS and allclose(atol=ATOL,
-rtol=RTOL) per tensor; dn / db by relative error.
+Pass bar, per tensor, against the unrounded fp64 oracle:
+  * every element: |got - ref| <= max(MAX_ABS, ulp(ref)), where ulp is one unit
+    in the last place of the output dtype at |ref| -- 2e-2 everywhere bf16 can
+    represent it (|ref| < 4), one bf16 ulp above that (0.03125 on [4, 8));
+  * allclose(atol=2e-2, rtol=5e-2) against the oracle rounded to the output
+    dtype, the reference harness's own criterion
+    (training/train/train_ssa_triton/check_ssa_triton_parity.py:124-149,206,
+    219-237, tolerances :1060-1069);
+  * dn / db: |got - ref| <= 2e-3 + 2e-2 |ref| (the reference's scalar bar).
+The reported "max_abs" is the plain maximum |got - ref|.
 """
 
 from __future__ import annotations
@@ -45,21 +49,37 @@ def make_inputs(B, Hq, Hkv, N, D, dtype, device, layout="contig", seed=1234, qkv
     return q, k, v, do
 
 
-def oracle_fwd_bwd(q, k, v, do, scale, n, b, causal):
-    """fp64 oracle on the CPU copies of (already rounded) kernel inputs."""
-    c = lambda t: t.detach().float().cpu().numpy().astype(np.float64)  # noqa: E731
-    return so.ssa_forward_backward(c(q), c(k), c(v), c(do), scale, n, b, causal)
+def _np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def oracle_fwd_bwd(q, k, v, do, scale, n, b, causal, out_for_delta=None):
+    """fp64 oracle on the CPU copies of (already rounded) kernel inputs.
+
+    ``out_for_delta``: the kernel's forward output, when the backward is to be
+    checked as the kernel-level function of (q, k, v, out, dout, m).
+    """
+    ofd = None if out_for_delta is None else _np64(out_for_delta)
+    return so.ssa_forward_backward(_np64(q), _np64(k), _np64(v), _np64(do), scale, n, b, causal, ofd)
+
+
+def ulp(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """One unit in the last place of `dtype` at |x| (normal range)."""
+    mant = {torch.bfloat16: 7, torch.float16: 10}.get(dtype, 23)
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
+    return torch.pow(2.0, e - mant)
 
 
 def tensor_err(got: torch.Tensor, ref: np.ndarray) -> dict:
     g = got.detach().float().cpu()
     r = torch.from_numpy(np.ascontiguousarray(ref)).float()
     r_round = r.to(got.dtype).float() if got.dtype in (torch.bfloat16, torch.float16) else r
-    d = (g - r_round).abs()
     d_raw = (g - r).abs()
+    bound = torch.maximum(torch.full_like(r, MAX_ABS), ulp(r, got.dtype))
     return {
-        "max_abs": float(d.max()) if d.numel() else 0.0,
-        "max_abs_vs_unrounded": float(d_raw.max()) if d.numel() else 0.0,
+        "max_abs": float(d_raw.max()) if d_raw.numel() else 0.0,
+        "max_abs_vs_rounded": float((g - r_round).abs().max()) if d_raw.numel() else 0.0,
+        "within_bound": bool((d_raw <= bound).all()),
         "rel_rmse": float(torch.sqrt(((g - r) ** 2).mean()) / (torch.sqrt((r ** 2).mean()) + 1e-12)),
         "allclose": bool(torch.allclose(g, r_round, atol=ATOL, rtol=RTOL)),
         "finite": bool(torch.isfinite(g).all()),
@@ -78,23 +98,21 @@ def scalar_err(got, ref: float) -> dict:
     }
 
 
-def compare(outs: dict, ref: dict, names=("out", "dq", "dk", "dv")) -> dict:
+def compare(outs: dict, ref: dict, names=("out", "dq", "dk", "dv"), scalars=("dn", "db")) -> dict:
     res = {name: tensor_err(outs[name], ref[name]) for name in names if name in outs}
-    for name in ("dn", "db"):
+    for name in scalars:
         if name in outs:
             res[name] = scalar_err(outs[name], ref[name])
     return res
 
 
-def assert_parity(res: dict, label: str, check_db: bool = True) -> None:
+def assert_parity(res: dict, label: str) -> None:
     for name, st in res.items():
         if name in ("dn", "db"):
-            if name == "db" and not check_db:
-                continue
             assert st["allclose"], f"{label}: {name} {st}"
             continue
         assert st["finite"], f"{label}: {name} has non-finite values"
-        assert st["max_abs"] <= MAX_ABS, f"{label}: {name} max_abs {st['max_abs']:.3e} > {MAX_ABS} ({st})"
+        assert st["within_bound"], f"{label}: {name} exceeds max(2e-2, 1 ulp) ({st})"
         assert st["allclose"], f"{label}: {name} not allclose ({st})"
 
 

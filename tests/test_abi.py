@@ -1,0 +1,130 @@
+"""C-ABI checks that need no GPU: exports, status strings, host-side validation.
+
+Validation runs on the host before any launch (include/ssa_mi355x.h), so bad
+arguments return their status code here without touching a device.  The
+pointers used below are never dereferenced: every call is rejected first.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from SSA import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def _declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*([a-z_][a-z0-9_]*)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_the_bound_symbols():
+    assert HEADERS, "no public header under include/"
+    assert _declared_functions() == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"libssa_mi355x.so does not export {name}"
+    assert lib.ssa_abi_version() == _lib.ABI_VERSION
+
+
+def test_status_strings():
+    for code in range(8):
+        assert _lib.status_text(code)
+    assert _lib.status_text(99) == "unknown status"
+
+
+def test_partials_count():
+    lib = _lib.lib()
+    assert lib.ssa_bwd_partials_count(4, 16, 4096) == 2 * 4 * 16 * 32
+    assert lib.ssa_bwd_partials_count(1, 1, 129) == 2 * 2
+    assert lib.ssa_bwd_partials_count(0, 1, 1) == 0
+
+
+FAKE = 0x10000  # 16-byte aligned, never dereferenced
+
+
+def _fwd_args(**kw):
+    t = _lib.Tensor4(FAKE, 8 * 128 * 64, 8 * 128, 128)
+    a = _lib.FwdArgs(t, t, t, t, FAKE, FAKE, FAKE, 1, 8, 8, 64, 128, _lib.SSA_DTYPE_BF16, 1, 0.088)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _bwd_args(**kw):
+    t = _lib.Tensor4(FAKE, 8 * 128 * 64, 8 * 128, 128)
+    a = _lib.BwdArgs(t, t, t, t, t, t, t, t, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                     1, 8, 8, 64, 128, _lib.SSA_DTYPE_BF16, 1, 0.088)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "field,value,status",
+    [
+        ("heads_kv", 3, _lib.SSA_ERR_SHAPE),        # Hq % Hkv != 0
+        ("batch", 0, _lib.SSA_ERR_SHAPE),
+        ("seqlen", 0, _lib.SSA_ERR_SHAPE),
+        ("head_dim", 96, _lib.SSA_ERR_HEAD_DIM),
+        ("head_dim", 256, _lib.SSA_ERR_HEAD_DIM),
+        ("dtype", 7, _lib.SSA_ERR_DTYPE),
+        ("m", None, _lib.SSA_ERR_NULL_POINTER),
+        ("ssa_n", None, _lib.SSA_ERR_NULL_POINTER),
+        ("q", _lib.Tensor4(FAKE + 2, 0, 0, 128), _lib.SSA_ERR_ALIGNMENT),
+        ("k", _lib.Tensor4(FAKE, 0, 0, 100), _lib.SSA_ERR_ALIGNMENT),
+        ("v", _lib.Tensor4(None, 0, 0, 128), _lib.SSA_ERR_NULL_POINTER),
+    ],
+)
+def test_fwd_validation(field, value, status):
+    a = _fwd_args(**{field: value})
+    assert _lib.lib().ssa_fwd(ctypes.byref(a), None) == status
+
+
+def test_fwd_null_args():
+    assert _lib.lib().ssa_fwd(None, None) == _lib.SSA_ERR_NULL_POINTER
+
+
+@pytest.mark.parametrize("entry", ["ssa_bwd", "ssa_bwd_dkdv", "ssa_bwd_dq", "ssa_bwd_reduce"])
+@pytest.mark.parametrize(
+    "field,value,status",
+    [
+        ("heads_kv", 5, _lib.SSA_ERR_SHAPE),
+        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),
+        ("dtype", 2, _lib.SSA_ERR_DTYPE),
+        ("partials", None, _lib.SSA_ERR_NULL_POINTER),
+        ("dn", None, _lib.SSA_ERR_NULL_POINTER),
+        ("dq", _lib.Tensor4(FAKE, 4, 0, 128), _lib.SSA_ERR_ALIGNMENT),
+    ],
+)
+def test_bwd_validation(entry, field, value, status):
+    a = _bwd_args(**{field: value})
+    assert getattr(_lib.lib(), entry)(ctypes.byref(a), None) == status
+
+
+def test_preprocess_validation_needs_only_out_dout_delta():
+    a = _bwd_args(q=_lib.Tensor4(None, 0, 0, 0), partials=None, dn=None, head_dim=48)
+    assert _lib.lib().ssa_bwd_preprocess(ctypes.byref(a), None) == _lib.SSA_ERR_HEAD_DIM
+    a = _bwd_args(delta=None)
+    assert _lib.lib().ssa_bwd_preprocess(ctypes.byref(a), None) == _lib.SSA_ERR_NULL_POINTER
+
+
+def test_status_maps_to_python_exceptions():
+    with pytest.raises(ValueError, match="head_dim"):
+        _lib.check(_lib.SSA_ERR_HEAD_DIM, "ssa_fwd")
+    with pytest.raises(RuntimeError, match="launch"):
+        _lib.check(_lib.SSA_ERR_LAUNCH, "ssa_fwd")
+    _lib.check(_lib.SSA_OK, "ssa_fwd")

@@ -256,3 +256,24 @@ def test_pair_counts():
     assert so.causal_pairs(1, 16, 16384) == 2_147_614_720
     assert so.causal_pairs(1, 4, 256) == 131_584
     assert so.varlen_pairs([0, 3, 5], 2) == 2 * (6 + 3)
+
+
+def test_out_for_delta_only_moves_delta_terms():
+    # dV does not depend on Delta; with the exact out the results are identical;
+    # Delta = rowsum(P * dP) when out is exact (softmax-backward identity).
+    rng = np.random.default_rng(12)
+    q, k, v, do = (_rand(rng, 1, 2, 20, 8), _rand(rng, 1, 2, 20, 8), _rand(rng, 1, 2, 20, 8),
+                   _rand(rng, 1, 2, 20, 8))
+    r = so.ssa_forward_backward(q, k, v, do, 0.3, 1.5, 0.8, True)
+    r_same = so.ssa_forward_backward(q, k, v, do, 0.3, 1.5, 0.8, True, out_for_delta=r["out"])
+    for name in ("dq", "dk", "dv", "delta"):
+        np.testing.assert_array_equal(r[name], r_same[name])
+    pert = r["out"] + 1e-3 * rng.standard_normal(r["out"].shape)
+    r_p = so.ssa_forward_backward(q, k, v, do, 0.3, 1.5, 0.8, True, out_for_delta=pert)
+    np.testing.assert_array_equal(r["dv"], r_p["dv"])
+    assert not np.allclose(r["dq"], r_p["dq"], rtol=0, atol=1e-9)
+    s = 0.3 * q @ k.swapaxes(-1, -2)
+    t = np.where(np.tril(np.ones((20, 20), bool)), so.ssa_logits(s, 1.5, 0.8), -np.inf)
+    p = np.exp(t - t.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    np.testing.assert_allclose(r["delta"], np.sum(p * (do @ v.swapaxes(-1, -2)), -1), rtol=1e-12, atol=1e-12)
