@@ -4,11 +4,12 @@
 // (training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:40-260).
 //
 // One workgroup = 4 waves = 128 query rows of one (batch, q-head); each wave
-// owns 32 query rows.  K/V tiles of 64 keys are staged through LDS and shared
-// by the 4 waves.  Everything is computed transposed so that a query row lives
-// in a single lane pair (l, l+32):
+// owns 32 query rows.  K/V tiles of 64 keys are double-buffered in LDS,
+// filled by direct-to-LDS loads and shared by the 4 waves (one barrier per
+// tile).  Everything is computed transposed so that a query row lives in a
+// single lane pair (l, l+32):
 //   S^T = K Q^T      (A = K rows from LDS, B = Q^T fragment held in registers)
-//   O^T += V^T P^T   (A = V^T gathered from LDS, B = P^T straight from S^T)
+//   O^T += V^T P^T   (A = V^T via LDS transpose reads, B = P^T straight from S^T)
 // Row max / row sum therefore need one exchange between the two wave halves.
 //
 // SSA transform in base 2: t2 = n * sign(s) * log2(1 + b|s|) = t / ln 2, with
@@ -16,43 +17,94 @@
 // decreasing for n < 0), the row max of t2 is t2 at the row max (or min) of
 // s, so the max is taken on the raw scores and p = exp2(n * sL - m) is a
 // single fma + exp.  The running max moves lazily (kRescaleTau); the stored
-// normaliser M = m + log2(l) is exact either way.
+// normaliser M = m + log2(l) is exact either way.  Masks are evaluated only on
+// the diagonal tile and the sequence-end tile.
+#include <type_traits>
+
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
+#include "ssa_tile.hpp"
 
 namespace ssa {
 
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void ssa_fwd_kernel(FwdParams p) {
-  constexpr int BM = 128, BN = 64, LDSD = D + 8;
-  constexpr int ND16 = D / 16, ND32 = D / 32;
-  constexpr int CH_PER_ROW = D / 8;              // 16-byte chunks per row
-  constexpr int CH_PER_T = BN * CH_PER_ROW / 256;  // chunks per thread per tile
-  typedef typename Vec8<T>::type v8;
+namespace {
 
-  __shared__ __attribute__((aligned(16))) T k_lds[BN * LDSD];
-  __shared__ __attribute__((aligned(16))) T v_lds[BN * LDSD];
+template <typename T, int D>
+struct FwdTile {
+  typedef typename Vec8<T>::type v8;
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  static constexpr int ND16 = D / 16, ND32 = D / 32;
+
+  // S^T for the 64 keys of the tile at `kl` (LDS byte address), blocks kb
+  // that are not `active` are skipped.
+  __device__ static __forceinline__ void scores(uint32_t kl, const v8* qf, int l32, int hh, const bool* active,
+                                                f32x16* s) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x16{};
+      if (!active[kb]) continue;
+#pragma unroll
+      for (int ds = 0; ds < ND16; ++ds) {
+        const v8 a = tile_read16<D, v8>(kl, kb * 32 + l32, 2 * ds + hh);
+        s[kb] = mfma32(a, qf[ds], s[kb]);
+      }
+    }
+  }
+
+  __device__ static __forceinline__ void pv(uint32_t vl, const v8 (*pb)[2], int lane, int hh, const bool* active,
+                                            f32x16* acc) {
+    const int g = lane >> 4, i = lane & 15;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if (!active[kb]) continue;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int rbase = kb * 32 + ks * 16 + 4 * hh;
+#pragma unroll
+        for (int db = 0; db < ND32; ++db) {
+          const int dgrp = db * 32 + (g & 1) * 16;
+          const v4 lo = tile_read_tr<D, v4>(vl, rbase, dgrp, i);
+          const v4 hi = tile_read_tr<D, v4>(vl, rbase + 8, dgrp, i);
+          const v8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[db] = mfma32(va, pb[kb][ks], acc[db]);
+        }
+      }
+    }
+  }
+};
+
+template <typename T, int D, bool CAUSAL, bool NPOS>
+__device__ __forceinline__ void fwd_body(const FwdParams& p, const int N, const int bh, const int qb, const int b,
+                                         const int h, const int hk, char* smem) {
+  typedef FwdTile<T, D> FT;
+  typedef typename FT::v8 v8;
+  constexpr int BM = 128, BN = 64;
+  constexpr int TILE_BYTES = BN * D * 2;
+  constexpr int ND16 = D / 16, ND32 = D / 32;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hh = lane >> 5;
-  const int nqb = (p.N + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = L / nqb;
-  const int qb = nqb - 1 - (L % nqb);  // heaviest (last) query block first
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h / (p.Hq / p.Hkv);
-
+  const uint32_t lds0 = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)(smem)));
+  // buffer t: K at lds0 + t*2*TILE_BYTES, V right after
   const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + h * p.q.sh;
-  const T* kg = static_cast<const T*>(p.k.ptr) + b * p.k.sb + hk * p.k.sh;
-  const T* vg = static_cast<const T*>(p.v.ptr) + b * p.v.sb + hk * p.v.sh;
+  const char* kg = static_cast<const char*>(p.k.ptr) + (b * p.k.sb + hk * p.k.sh) * 2;
+  const char* vg = static_cast<const char*>(p.v.ptr) + (b * p.v.sb + hk * p.v.sh) * 2;
   T* og = static_cast<T*>(const_cast<void*>(p.o.ptr)) + b * p.o.sb + h * p.o.sh;
 
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;  // u = c * |q.k|
-  const float sgn = n >= 0.f ? 1.f : -1.f;
-  const int N = p.N;
   const int q0 = qb * BM;
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
+
+  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
+  // first tile that needs masks: the causal diagonal or the sequence end
+  const int nfull = CAUSAL ? min(q0 / BN, N / BN) : N / BN;
+
+  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, lane);
+  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, lane);
 
   v8 qf[ND16];
 #pragma unroll
@@ -64,72 +116,45 @@ __global__ __launch_bounds__(256) void ssa_fwd_kernel(FwdParams p) {
   for (int i = 0; i < ND32; ++i) acc[i] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
-
-  u32x4 kreg[CH_PER_T], vreg[CH_PER_T];
-  auto gload = [&](int tile) {
-#pragma unroll
-    for (int i = 0; i < CH_PER_T; ++i) {
-      const int ch = tid + i * 256;
-      const int row = ch / CH_PER_ROW, col = (ch % CH_PER_ROW) * 8;
-      const int key = tile * BN + row;
-      if (key < N) {
-        kreg[i] = *reinterpret_cast<const u32x4*>(kg + key * p.k.ss + col);
-        vreg[i] = *reinterpret_cast<const u32x4*>(vg + key * p.v.ss + col);
-      } else {
-        kreg[i] = u32x4{0u, 0u, 0u, 0u};
-        vreg[i] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-
-  gload(0);
-  for (int t = 0; t < ntiles; ++t) {
+  auto tile = [&](int t, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < CH_PER_T; ++i) {
-      const int ch = tid + i * 256;
-      const int row = ch / CH_PER_ROW, col = (ch % CH_PER_ROW) * 8;
-      *reinterpret_cast<u32x4*>(&k_lds[row * LDSD + col]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&v_lds[row * LDSD + col]) = vreg[i];
+    const uint32_t kl = lds0 + (t & 1) * 2 * TILE_BYTES;
+    const uint32_t vl = kl + TILE_BYTES;
+    if (t + 1 < ntiles) {
+      const uint32_t nk = lds0 + ((t + 1) & 1) * 2 * TILE_BYTES;
+      tile_load_async<D, BN, 4>(kg, p.k.ss, (t + 1) * BN, N, nk, wave, lane);
+      tile_load_async<D, BN, 4>(vg, p.v.ss, (t + 1) * BN, N, nk + TILE_BYTES, wave, lane);
     }
-    __syncthreads();
-    if (t + 1 < ntiles) gload(t + 1);
-
     const int kbase = t * BN;
     bool active[2];
-    f32x16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kstart = kbase + kb * 32;
-      active[kb] = kstart < N && (!CAUSAL || kstart <= wq0 + 31);
-      s[kb] = f32x16{};
-      if (active[kb]) {
-#pragma unroll
-        for (int ds = 0; ds < ND16; ++ds) {
-          const v8 a = load16<v8>(&k_lds[(kb * 32 + l32) * LDSD + ds * 16 + 8 * hh]);
-          s[kb] = mfma32(a, qf[ds], s[kb]);
-        }
-      }
+      active[kb] = !MASKED || (kstart < N && (!CAUSAL || kstart <= wq0 + 31));
     }
+    f32x16 s[2];
+    FT::scores(kl, qf, l32, hh, active, s);
 
-    // Row max over valid keys, on sgn * s (monotone image of t2).
-    float zmax = -INFINITY;
+    // Row extreme of the raw scores over valid keys (max for n >= 0, min for n < 0).
+    float z = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      if (!active[kb]) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kbase + kb * 32 + crow(r, hh);
-        const bool valid = key < N && (!CAUSAL || key <= qrow);
-        if (valid) zmax = fmaxf(zmax, sgn * s[kb][r]);
+        if (MASKED) {
+          const int key = kbase + kb * 32 + crow(r, hh);
+          const bool valid = active[kb] && key < N && (!CAUSAL || key <= qrow);
+          if (!valid) s[kb][r] = NPOS ? -INFINITY : INFINITY;
+        }
+        z = fmaxf(z, NPOS ? s[kb][r] : -s[kb][r]);
       }
     }
-    zmax = fmaxf(zmax, swap_halves(zmax));
+    z = fmaxf(z, swap_halves(z));
     float t2max = -INFINITY;
-    if (zmax != -INFINITY) {
-      const float sst = sgn * zmax;
+    if (z != -INFINITY) {
+      const float sst = NPOS ? z : -z;
       t2max = n * copysignf(fast_log2(fmaf(c, fabsf(sst), 1.f)), sst);
     }
     if (__any(t2max > m_run + kRescaleTau)) {
@@ -140,40 +165,25 @@ __global__ __launch_bounds__(256) void ssa_fwd_kernel(FwdParams p) {
       l_run *= alpha;
       m_run = mnew;
     }
+    const float neg_m = -m_run;
 
     v8 pb[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kbase + kb * 32 + crow(r, hh);
-        const bool valid = active[kb] && key < N && (!CAUSAL || key <= qrow);
         const float x = s[kb][r];
         const float sl = copysignf(fast_log2(fmaf(c, fabsf(x), 1.f)), x);
-        const float pv = valid ? fast_exp2(fmaf(n, sl, -m_run)) : 0.f;
+        float pv = fast_exp2(fmaf(n, sl, neg_m));
+        if (MASKED) pv = (NPOS ? x == -INFINITY : x == INFINITY) ? 0.f : pv;
         l_run += pv;
         pb[kb][r >> 3][r & 7] = static_cast<T>(pv);
       }
     }
-
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      if (!active[kb]) continue;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int db = 0; db < ND32; ++db) {
-          v8 va;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int krow = kb * 32 + ks * 16 + crow(e, hh);
-            va[e] = v_lds[krow * LDSD + db * 32 + l32];
-          }
-          acc[db] = mfma32(va, pb[kb][ks], acc[db]);
-        }
-      }
-    }
-  }
+    FT::pv(vl, pb, lane, hh, active, acc);
+  };
+  for (int t = 0; t < nfull; ++t) tile(t, std::false_type{});
+  for (int t = nfull; t < ntiles; ++t) tile(t, std::true_type{});
 
   const float l_tot = l_run + swap_halves(l_run);
   const float l_safe = l_tot > 0.f ? l_tot : 1.f;
@@ -184,16 +194,33 @@ __global__ __launch_bounds__(256) void ssa_fwd_kernel(FwdParams p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = db * 32 + g * 8 + 4 * hh;
-        T* dst = og + qrow * p.o.ss + d0;
         typedef T t4 __attribute__((ext_vector_type(4)));
         t4 o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o4[e] = static_cast<T>(acc[db][4 * g + e] * inv);
-        *reinterpret_cast<t4*>(dst) = o4;
+        *reinterpret_cast<t4*>(og + qrow * p.o.ss + d0) = o4;
       }
     }
     if (hh == 0) p.m[static_cast<int64_t>(bh) * N + qrow] = m_run + log2f(l_safe);
   }
+}
+
+}  // namespace
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void ssa_fwd_kernel(FwdParams p) {
+  constexpr int BM = 128;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * 64 * D * 2];
+  const int N = p.N;
+  const int nqb = (N + BM - 1) / BM;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = L / nqb;
+  const int qb = nqb - 1 - (L % nqb);  // heaviest (last) query block first
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h / (p.Hq / p.Hkv);
+  if (*p.n_ptr >= 0.f)
+    fwd_body<T, D, CAUSAL, true>(p, N, bh, qb, b, h, hk, smem);
+  else
+    fwd_body<T, D, CAUSAL, false>(p, N, bh, qb, b, h, hk, smem);
 }
 
 template <typename T, int D, bool CAUSAL>
