@@ -16,8 +16,11 @@
 //   dV_j += P dO_i,  dK_j += scale n b dS' q_i,  dQ_i += scale n b dS' k_j
 //   dn  += ln2 * dT sL,  db += n scale dS' (q_i.k_j)
 // The constant factors (scale n b, ln2, n scale) are applied once at the end.
+#include <type_traits>
+
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
+#include "ssa_tile.hpp"
 
 namespace ssa {
 
@@ -51,25 +54,26 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_kernel(BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // dK, dV for a block of 128 keys (32 per wave) of one (batch, kv-head), looping
-// over every q-head of the GQA group and every 32-query tile at or after the
-// keys (causal).  S = Q K^T is computed with the keys on the lane axis, so
+// over every q-head of the GQA group and every 32-query sub-tile at or after
+// the keys (causal).  S = Q K^T is computed with the keys on the lane axis, so
 // P^T and dS'^T come out of the accumulators already in A-operand order for
-// dV += P^T dO and dK += dS'^T Q.
+// dV += P^T dO and dK += dS'^T Q; the B operands (dO, Q with the query index
+// as the contraction dimension) are LDS transpose reads of the same sub-tiles
+// the S and dP products read row-wise.  K and V stay in registers.  The
+// sub-tiles (Q, dO, M, Delta) are double-buffered in LDS by direct loads.
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void ssa_bwd_dkdv_kernel(BwdParams p) {
-  constexpr int BN = 128, BMQ = 32, LDSD = D + 8;
-  constexpr int ND16 = D / 16, ND32 = D / 32;
-  constexpr int CH_PER_ROW = D / 8;
-  constexpr int CH = BMQ * CH_PER_ROW;
+__global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
-
-  __shared__ __attribute__((aligned(16))) T q_lds[BMQ * LDSD];
-  __shared__ __attribute__((aligned(16))) T do_lds[BMQ * LDSD];
-  __shared__ float m_lds[BMQ], dl_lds[BMQ];
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  constexpr int BN = 128, BMQ = 32;
+  constexpr int ND16 = D / 16, ND32 = D / 32;
+  constexpr int TILE = BMQ * D * 2;   // one Q (or dO) sub-tile
+  constexpr int BUF = 2 * TILE + 256;  // Q, dO, M[32], Delta[32]
+  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
   __shared__ float red[2][4];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hh = lane >> 5;
+  const int l32 = lane & 31, hh = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
   const int N = p.N;
   const int nkb = dkdv_key_blocks(N);
   const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -77,14 +81,34 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const int kb = L % nkb;  // ascending = heaviest first under causal
   const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
   const int G = p.Hq / p.Hkv;
-
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;
+  const uint32_t lds0 = lds_addr(smem);
 
-  const int k0w = kb * BN + wave * 32;
+  const int k0 = kb * BN;
+  const int k0w = k0 + wave * 32;
   const int key = k0w + l32;
   const T* kg = static_cast<const T*>(p.k.ptr) + b * p.k.sb + hk * p.k.sh;
   const T* vg = static_cast<const T*>(p.v.ptr) + b * p.v.sb + hk * p.v.sh;
+
+  const int qstart = CAUSAL ? k0 : 0;
+  const int nsub = (N - qstart + BMQ - 1) / BMQ;
+  const int nsteps = G * nsub;
+  const bool key_edge = k0 + BN > N;
+
+  auto issue = [&](int st, uint32_t buf) {
+    const int g = st / nsub, q0 = qstart + (st % nsub) * BMQ;
+    const int hq = hk * G + g;
+    const char* qg = static_cast<const char*>(p.q.ptr) + (b * p.q.sb + hq * p.q.sh) * 2;
+    const char* dog = static_cast<const char*>(p.dout.ptr) + (b * p.dout.sb + hq * p.dout.sh) * 2;
+    tile_load_async<D, BMQ, 4>(qg, p.q.ss, q0, N, buf, wave, lane);
+    tile_load_async<D, BMQ, 4>(dog, p.dout.ss, q0, N, buf + TILE, wave, lane);
+    if (wave == 3) {
+      const int64_t rb = (static_cast<int64_t>(b) * p.Hq + hq) * N;
+      pair32_load_async(p.m + rb, p.delta + rb, q0, N, buf + 2 * TILE, lane);
+    }
+  };
+  issue(0, lds0);
 
   v8 kf[ND16], vf[ND16];
 #pragma unroll
@@ -101,87 +125,80 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_kernel(BwdParams p) {
   }
   float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;
 
-  for (int g = 0; g < G; ++g) {
-    const int hq = hk * G + g;
-    const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + hq * p.q.sh;
-    const T* dog = static_cast<const T*>(p.dout.ptr) + b * p.dout.sb + hq * p.dout.sh;
-    const float* mg = p.m + (static_cast<int64_t>(b) * p.Hq + hq) * N;
-    const float* dlg = p.delta + (static_cast<int64_t>(b) * p.Hq + hq) * N;
-    const int qstart = CAUSAL ? kb * BN : 0;
-    for (int q0 = qstart; q0 < N; q0 += BMQ) {
-      __syncthreads();
-      for (int ch = tid; ch < CH; ch += 256) {
-        const int row = ch / CH_PER_ROW, col = (ch % CH_PER_ROW) * 8;
-        const int qi = q0 + row;
-        u32x4 a = u32x4{0u, 0u, 0u, 0u}, d = u32x4{0u, 0u, 0u, 0u};
-        if (qi < N) {
-          a = *reinterpret_cast<const u32x4*>(qg + qi * p.q.ss + col);
-          d = *reinterpret_cast<const u32x4*>(dog + qi * p.dout.ss + col);
-        }
-        *reinterpret_cast<u32x4*>(&q_lds[row * LDSD + col]) = a;
-        *reinterpret_cast<u32x4*>(&do_lds[row * LDSD + col]) = d;
-      }
-      if (tid < BMQ) {
-        const int qi = q0 + tid;
-        m_lds[tid] = qi < N ? mg[qi] : 0.f;
-        dl_lds[tid] = qi < N ? dlg[qi] : 0.f;
-      }
-      __syncthreads();
-      if (k0w >= N) continue;
-      if (CAUSAL && q0 + BMQ - 1 < k0w) continue;
-
-      f32x16 s = f32x16{}, dp = f32x16{};
+  auto body = [&](uint32_t buf, int q0, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    const uint32_t ql = buf, dl = buf + TILE, ml = buf + 2 * TILE;
+    f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-      for (int ds = 0; ds < ND16; ++ds) {
-        const v8 qa = load16<v8>(&q_lds[l32 * LDSD + ds * 16 + 8 * hh]);
-        const v8 da = load16<v8>(&do_lds[l32 * LDSD + ds * 16 + 8 * hh]);
-        s = mfma32(qa, kf[ds], s);
-        dp = mfma32(da, vf[ds], dp);
-      }
-
-      v8 pa[2], sa[2];
-      float tdn = 0.f, tdb = 0.f;
+    for (int ds = 0; ds < ND16; ++ds) {
+      const v8 qa = tile_read16<D, v8>(ql, l32, 2 * ds + hh);
+      const v8 da = tile_read16<D, v8>(dl, l32, 2 * ds + hh);
+      s = mfma32(qa, kf[ds], s);
+      dp = mfma32(da, vf[ds], dp);
+    }
+    v8 pa[2], sa[2];
+    float tdn = 0.f, tdb = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qo = crow(r, hh);
-        const int qi = q0 + qo;
-        const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
+    for (int j = 0; j < 4; ++j) {
+      const f32x4_t mv = lds_read_f4(ml + (8 * j + 4 * hh) * 4);
+      const f32x4_t dv4 = lds_read_f4(ml + 128 + (8 * j + 4 * hh) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * j + e;
         const float x = s[r];
         const float u1 = fmaf(c, fabsf(x), 1.f);
         const float sl = copysignf(fast_log2(u1), x);
-        const float pv = valid ? fast_exp2(fmaf(n, sl, -m_lds[qo])) : 0.f;
-        const float dt = pv * (dp[r] - dl_lds[qo]);
+        float pv = fast_exp2(fmaf(n, sl, -mv[e]));
+        if (MASKED) {
+          const int qi = q0 + crow(r, hh);
+          const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
+          pv = valid ? pv : 0.f;
+        }
+        const float dt = pv * (dp[r] - dv4[e]);
         const float dsp = dt * fast_rcp(u1);
         tdn = fmaf(dt, sl, tdn);
         tdb = fmaf(dsp, x, tdb);
         pa[r >> 3][r & 7] = static_cast<T>(pv);
         sa[r >> 3][r & 7] = static_cast<T>(dsp);
       }
-      {  // Kahan accumulation of the per-tile sums
-        const float y = tdn - dn_c, t = dn_acc + y;
-        dn_c = (t - dn_acc) - y;
-        dn_acc = t;
-        const float y2 = tdb - db_c, t2 = db_acc + y2;
-        db_c = (t2 - db_acc) - y2;
-        db_acc = t2;
-      }
-
+    }
+    {  // Kahan accumulation of the per-sub-tile sums
+      const float y = tdn - dn_c, t = dn_acc + y;
+      dn_c = (t - dn_acc) - y;
+      dn_acc = t;
+      const float y2 = tdb - db_c, t2 = db_acc + y2;
+      db_c = (t2 - db_acc) - y2;
+      db_acc = t2;
+    }
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < 2; ++ks) {
+      const int rbase = ks * 16 + 4 * hh;
 #pragma unroll
-        for (int db = 0; db < ND32; ++db) {
-          v8 dob, qbv;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int qrow = ks * 16 + crow(e, hh);
-            dob[e] = do_lds[qrow * LDSD + db * 32 + l32];
-            qbv[e] = q_lds[qrow * LDSD + db * 32 + l32];
-          }
-          dv[db] = mfma32(pa[ks], dob, dv[db]);
-          dk[db] = mfma32(sa[ks], qbv, dk[db]);
-        }
+      for (int db = 0; db < ND32; ++db) {
+        const int dgrp = db * 32 + (g16 & 1) * 16;
+        const v4 dlo = tile_read_tr<D, v4>(dl, rbase, dgrp, i16);
+        const v4 dhi = tile_read_tr<D, v4>(dl, rbase + 8, dgrp, i16);
+        const v4 qlo = tile_read_tr<D, v4>(ql, rbase, dgrp, i16);
+        const v4 qhi = tile_read_tr<D, v4>(ql, rbase + 8, dgrp, i16);
+        dv[db] = mfma32(pa[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7), dv[db]);
+        dk[db] = mfma32(sa[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7), dk[db]);
       }
     }
+  };
+
+  for (int st = 0; st < nsteps; ++st) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const uint32_t buf = lds0 + (st & 1) * BUF;
+    if (st + 1 < nsteps) issue(st + 1, lds0 + ((st + 1) & 1) * BUF);
+    const int q0 = qstart + (st % nsub) * BMQ;
+    if (k0w >= N) continue;
+    if (CAUSAL && q0 + BMQ - 1 < k0w) continue;
+    const bool masked = key_edge || q0 + BMQ > N || (CAUSAL && q0 < k0 + BN);
+    if (masked)
+      body(buf, q0, std::true_type{});
+    else
+      body(buf, q0, std::false_type{});
   }
 
   // Store dK (scaled by scale * n * b) and dV: lane holds d = 32*db + l32,
@@ -223,39 +240,46 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ for 128 query rows (32 per wave) of one (batch, q-head): the forward's
-// transposed layout (query on the lane axis), K/V tiles of 64 keys in LDS,
-// dQ^T += K^T dS'^T with K^T gathered from the K tile.
+// dQ for 128 query rows (32 per wave) of one (batch, q-head), laid out like
+// the forward (query on the lane axis): S^T = K Q^T and dP^T = V dO^T with K/V
+// rows read from double-buffered LDS tiles, dQ^T += K^T dS'^T with K^T from
+// LDS transpose reads of the same K tile.  Q and dO stay in registers.
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void ssa_bwd_dq_kernel(BwdParams p) {
-  constexpr int BM = 128, BN = 64, LDSD = D + 8;
-  constexpr int ND16 = D / 16, ND32 = D / 32;
-  constexpr int CH_PER_ROW = D / 8;
-  constexpr int CH_PER_T = BN * CH_PER_ROW / 256;
+__global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
-
-  __shared__ __attribute__((aligned(16))) T k_lds[BN * LDSD];
-  __shared__ __attribute__((aligned(16))) T v_lds[BN * LDSD];
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  constexpr int BM = 128, BN = 64;
+  constexpr int ND16 = D / 16, ND32 = D / 32;
+  constexpr int TILE_BYTES = BN * D * 2;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * TILE_BYTES];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hh = lane >> 5;
+  const int l32 = lane & 31, hh = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
   const int N = p.N;
   const int nqb = (N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = L / nqb;
   const int qb = nqb - 1 - (L % nqb);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h / (p.Hq / p.Hkv);
+  const uint32_t lds0 = lds_addr(smem);
 
   const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + h * p.q.sh;
   const T* dog = static_cast<const T*>(p.dout.ptr) + b * p.dout.sb + h * p.dout.sh;
-  const T* kg = static_cast<const T*>(p.k.ptr) + b * p.k.sb + hk * p.k.sh;
-  const T* vg = static_cast<const T*>(p.v.ptr) + b * p.v.sb + hk * p.v.sh;
+  const char* kg = static_cast<const char*>(p.k.ptr) + (b * p.k.sb + hk * p.k.sh) * 2;
+  const char* vg = static_cast<const char*>(p.v.ptr) + (b * p.v.sb + hk * p.v.sh) * 2;
 
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;
   const int q0 = qb * BM;
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
+
+  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
+  const int nfull = CAUSAL ? min(q0 / BN, N / BN) : N / BN;
+
+  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, lane);
+  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, lane);
 
   v8 qf[ND16], dof[ND16];
 #pragma unroll
@@ -271,79 +295,60 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int i = 0; i < ND32; ++i) dq[i] = f32x16{};
 
-  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
-
-  u32x4 kreg[CH_PER_T], vreg[CH_PER_T];
-  auto gload = [&](int tile) {
-#pragma unroll
-    for (int i = 0; i < CH_PER_T; ++i) {
-      const int ch = tid + i * 256;
-      const int row = ch / CH_PER_ROW, col = (ch % CH_PER_ROW) * 8;
-      const int kk = tile * BN + row;
-      if (kk < N) {
-        kreg[i] = *reinterpret_cast<const u32x4*>(kg + kk * p.k.ss + col);
-        vreg[i] = *reinterpret_cast<const u32x4*>(vg + kk * p.v.ss + col);
-      } else {
-        kreg[i] = u32x4{0u, 0u, 0u, 0u};
-        vreg[i] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-
-  gload(0);
-  for (int t = 0; t < ntiles; ++t) {
+  auto tile = [&](int t, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < CH_PER_T; ++i) {
-      const int ch = tid + i * 256;
-      const int row = ch / CH_PER_ROW, col = (ch % CH_PER_ROW) * 8;
-      *reinterpret_cast<u32x4*>(&k_lds[row * LDSD + col]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&v_lds[row * LDSD + col]) = vreg[i];
+    const uint32_t kl = lds0 + (t & 1) * 2 * TILE_BYTES;
+    const uint32_t vl = kl + TILE_BYTES;
+    if (t + 1 < ntiles) {
+      const uint32_t nk = lds0 + ((t + 1) & 1) * 2 * TILE_BYTES;
+      tile_load_async<D, BN, 4>(kg, p.k.ss, (t + 1) * BN, N, nk, wave, lane);
+      tile_load_async<D, BN, 4>(vg, p.v.ss, (t + 1) * BN, N, nk + TILE_BYTES, wave, lane);
     }
-    __syncthreads();
-    if (t + 1 < ntiles) gload(t + 1);
-
     const int kbase = t * BN;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kstart = kbase + kb * 32;
-      if (kstart >= N || (CAUSAL && kstart > wq0 + 31)) continue;
+      if (MASKED && (kstart >= N || (CAUSAL && kstart > wq0 + 31))) continue;
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int ds = 0; ds < ND16; ++ds) {
-        const v8 ka = load16<v8>(&k_lds[(kb * 32 + l32) * LDSD + ds * 16 + 8 * hh]);
-        const v8 va = load16<v8>(&v_lds[(kb * 32 + l32) * LDSD + ds * 16 + 8 * hh]);
+        const v8 ka = tile_read16<D, v8>(kl, kb * 32 + l32, 2 * ds + hh);
+        const v8 va = tile_read16<D, v8>(vl, kb * 32 + l32, 2 * ds + hh);
         s = mfma32(ka, qf[ds], s);
         dp = mfma32(va, dof[ds], dp);
       }
       v8 sb[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = kstart + crow(r, hh);
-        const bool valid = qrow < N && kk < N && (!CAUSAL || kk <= qrow);
         const float x = s[r];
         const float u1 = fmaf(c, fabsf(x), 1.f);
         const float sl = copysignf(fast_log2(u1), x);
-        const float pv = valid ? fast_exp2(fmaf(n, sl, -mq)) : 0.f;
+        float pv = fast_exp2(fmaf(n, sl, -mq));
+        if (MASKED) {
+          const int kk = kstart + crow(r, hh);
+          const bool valid = qrow < N && kk < N && (!CAUSAL || kk <= qrow);
+          pv = valid ? pv : 0.f;
+        }
         const float dsp = pv * (dp[r] - dlq) * fast_rcp(u1);
         sb[r >> 3][r & 7] = static_cast<T>(dsp);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
+        const int rbase = kb * 32 + ks * 16 + 4 * hh;
 #pragma unroll
         for (int db = 0; db < ND32; ++db) {
-          v8 ka;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int krow = kb * 32 + ks * 16 + crow(e, hh);
-            ka[e] = k_lds[krow * LDSD + db * 32 + l32];
-          }
-          dq[db] = mfma32(ka, sb[ks], dq[db]);
+          const int dgrp = db * 32 + (g16 & 1) * 16;
+          const v4 lo = tile_read_tr<D, v4>(kl, rbase, dgrp, i16);
+          const v4 hi = tile_read_tr<D, v4>(kl, rbase + 8, dgrp, i16);
+          dq[db] = mfma32(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), sb[ks], dq[db]);
         }
       }
     }
-  }
+  };
+  for (int t = 0; t < nfull; ++t) tile(t, std::false_type{});
+  for (int t = nfull; t < ntiles; ++t) tile(t, std::true_type{});
 
   const float qscale = p.scale * n * *p.b_ptr;
   if (qrow < N) {
@@ -352,11 +357,10 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_kernel(BwdParams p) {
     for (int db = 0; db < ND32; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        typedef T t4 __attribute__((ext_vector_type(4)));
-        t4 o4;
+        v4 o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o4[e] = static_cast<T>(dq[db][4 * g + e] * qscale);
-        *reinterpret_cast<t4*>(dqg + db * 32 + g * 8 + 4 * hh) = o4;
+        *reinterpret_cast<v4*>(dqg + db * 32 + g * 8 + 4 * hh) = o4;
       }
     }
   }

@@ -34,13 +34,14 @@ struct TileLayout {
 
 // Issue the loads of one ROWS x D tile (rows row0.. of a [*, D] matrix with
 // row stride `ss` elements) into `lds` (byte address).  Called by all NW waves
-// of the workgroup; wave w issues instructions w, w + NW, ...
+// of the workgroup; wave w issues instructions w, w + NW, ... (a wave may
+// issue none when the tile has fewer 1 KB pieces than there are waves).
 template <int D, int ROWS, int NW>
 __device__ __forceinline__ void tile_load_async(const void* gbase, int64_t ss, int row0, int nrows, uint32_t lds,
                                                 int wave, int lane) {
   using TL = TileLayout<D>;
   constexpr int NINST = ROWS * TL::ROW_BYTES / 1024;
-  static_assert(NINST % NW == 0, "tile must split evenly over the waves");
+  static_assert(NINST * 1024 == ROWS * TL::ROW_BYTES, "tile must be a whole number of 1 KB pieces");
   const int rl = lane / TL::CPR, slot = lane % TL::CPR;
 #pragma unroll
   for (int j = wave; j < NINST; j += NW) {
@@ -72,6 +73,28 @@ __device__ __forceinline__ V4 tile_read_tr(uint32_t lds, int rbase, int dgrp, in
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
   const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(lds + off));
   return __builtin_bit_cast(V4, v);
+}
+
+// 32 consecutive fp32 values of each of two vectors (rows row0.. of `a` and of
+// `b`, clamped to nrows - 1) into 256 bytes of LDS at `lds`: a first, then b.
+// One global_load_lds_dword issued by the calling wave.
+__device__ __forceinline__ void pair32_load_async(const float* a, const float* b, int row0, int nrows, uint32_t lds,
+                                                  int lane) {
+  int r = row0 + (lane & 31);
+  r = r < nrows ? r : nrows - 1;
+  const float* src = (lane < 32 ? a : b) + r;
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(uintptr_t)(lds), 4, 0, 0);
+}
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t lds_read_f4(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(addr);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
 }
 
 }  // namespace ssa
