@@ -7,10 +7,12 @@ If it is missing, ``lib()`` raises: there is no CPU or PyTorch fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libssa_mi355x.so"
+# SSA_MI355X_LIB overrides the library path (e.g. to compare two builds).
+LIB_PATH = Path(os.environ.get("SSA_MI355X_LIB", str(Path(__file__).resolve().parent / "libssa_mi355x.so")))
 
 SSA_OK = 0
 SSA_ERR_NULL_POINTER = 1
