@@ -41,7 +41,9 @@ enum {
   SSA_ERR_SHAPE = 2,          /* bad batch/heads/seqlen (e.g. Hq % Hkv != 0)      */
   SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128                  */
   SSA_ERR_DTYPE = 4,          /* dtype not SSA_DTYPE_BF16 / SSA_DTYPE_FP16        */
-  SSA_ERR_ALIGNMENT = 5,      /* base pointer or stride not 16-byte aligned       */
+  SSA_ERR_ALIGNMENT = 5,      /* layout: base pointer not 16-byte aligned, a      */
+                              /* stride negative or not a multiple of 8, or the   */
+                              /* row stride >= 2^24 elements                      */
   SSA_ERR_LAUNCH = 6,         /* the HIP runtime rejected a kernel launch         */
   SSA_ERR_CU_SEQLENS = 7      /* varlen: bad document table                       */
 };

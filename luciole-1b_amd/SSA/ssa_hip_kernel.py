@@ -37,13 +37,19 @@ def _is_pow2(x: int) -> bool:
     return x > 0 and (x & (x - 1)) == 0
 
 
+_MAX_ROW_STRIDE = 1 << 24
+
+
 def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
-    """Return ``t`` or a contiguous copy so that stride(-1) == 1 and rows are 16-byte aligned."""
+    """Return ``t`` or a contiguous copy so that stride(-1) == 1, rows are 16-byte
+    aligned and the row stride is below 2**24 elements (the kernels' limit)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
         return t.contiguous()
     for dim in range(3):
         if t.shape[dim] > 1 and t.stride(dim) % 8 != 0:
             return t.contiguous()
+    if t.shape[2] > 1 and t.stride(2) >= _MAX_ROW_STRIDE:
+        return t.contiguous()
     return t
 
 

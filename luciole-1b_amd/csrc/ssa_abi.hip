@@ -19,6 +19,9 @@ int32_t check_tensor(const ssa_tensor4& t, bool required) {
   if (t.ptr == nullptr) return required ? SSA_ERR_NULL_POINTER : SSA_OK;
   if (!aligned16(t.ptr)) return SSA_ERR_ALIGNMENT;
   if ((t.stride_b % 8) != 0 || (t.stride_h % 8) != 0 || (t.stride_s % 8) != 0) return SSA_ERR_ALIGNMENT;
+  if (t.stride_b < 0 || t.stride_h < 0 || t.stride_s < 0) return SSA_ERR_ALIGNMENT;
+  // Tile loads address rows with 32-bit byte offsets from a per-tile base.
+  if (t.stride_s >= (1ll << 24)) return SSA_ERR_ALIGNMENT;
   return SSA_OK;
 }
 
@@ -95,7 +98,9 @@ const char* ssa_status_string(int32_t status) {
     case SSA_ERR_SHAPE: return "invalid shape (batch/heads/seqlen must be > 0 and Hq % Hkv == 0)";
     case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128)";
     case SSA_ERR_DTYPE: return "unsupported dtype (supported: bf16, fp16)";
-    case SSA_ERR_ALIGNMENT: return "tensor base pointer must be 16-byte aligned and strides multiples of 8 elements";
+    case SSA_ERR_ALIGNMENT:
+      return "unsupported tensor layout (base pointer 16-byte aligned, strides non-negative multiples of 8 "
+             "elements, row stride below 2^24 elements)";
     case SSA_ERR_LAUNCH: return "HIP kernel launch failed";
     case SSA_ERR_CU_SEQLENS: return "invalid cu_seqlens";
     default: return "unknown status";

@@ -72,8 +72,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
   __shared__ float red[2][4];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hh = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hh = lane >> 5;
   const int N = p.N;
   const int nkb = dkdv_key_blocks(N);
   const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -84,6 +85,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;
   const uint32_t lds0 = lds_addr(smem);
+  const RowBase<D> rb(l32, hh);
+  const TrBase<D> tb(lane);
+  const LoadLane llq(lane, wave, p.q.ss), lld(lane, wave, p.dout.ss);
 
   const int k0 = kb * BN;
   const int k0w = k0 + wave * 32;
@@ -101,8 +105,13 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const int hq = hk * G + g;
     const char* qg = static_cast<const char*>(p.q.ptr) + (b * p.q.sb + hq * p.q.sh) * 2;
     const char* dog = static_cast<const char*>(p.dout.ptr) + (b * p.dout.sb + hq * p.dout.sh) * 2;
-    tile_load_async<D, BMQ, 4>(qg, p.q.ss, q0, N, buf, wave, lane);
-    tile_load_async<D, BMQ, 4>(dog, p.dout.ss, q0, N, buf + TILE, wave, lane);
+    if (q0 + BMQ <= N) {
+      tile_load_pieces<D, BMQ, 4, false>(qg, p.q.ss, q0, N, buf, wave, llq);
+      tile_load_pieces<D, BMQ, 4, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
+    } else {
+      tile_load_pieces<D, BMQ, 4, true>(qg, p.q.ss, q0, N, buf, wave, llq);
+      tile_load_pieces<D, BMQ, 4, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
+    }
     if (wave == 3) {
       const int64_t rb = (static_cast<int64_t>(b) * p.Hq + hq) * N;
       pair32_load_async(p.m + rb, p.delta + rb, q0, N, buf + 2 * TILE, lane);
@@ -127,12 +136,13 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
 
   auto body = [&](uint32_t buf, int q0, auto masked_tag) {
     constexpr bool MASKED = decltype(masked_tag)::value;
-    const uint32_t ql = buf, dl = buf + TILE, ml = buf + 2 * TILE;
+    const uint32_t ml = buf + 2 * TILE;
+    const RowBase<D> rq = at_tile(rb, buf), rd = at_tile(rb, buf + TILE);
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < ND16; ++ds) {
-      const v8 qa = tile_read16<D, v8>(ql, l32, 2 * ds + hh);
-      const v8 da = tile_read16<D, v8>(dl, l32, 2 * ds + hh);
+      const v8 qa = tile_read_row<D, v8>(rq, 0, ds);
+      const v8 da = tile_read_row<D, v8>(rd, 0, ds);
       s = mfma32(qa, kf[ds], s);
       dp = mfma32(da, vf[ds], dp);
     }
@@ -170,16 +180,15 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       db_c = (t2 - db_acc) - y2;
       db_acc = t2;
     }
+    const TrBase<D> tq = at_tile(tb, buf), td = at_tile(tb, buf + TILE);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int rbase = ks * 16 + 4 * hh;
 #pragma unroll
       for (int db = 0; db < ND32; ++db) {
-        const int dgrp = db * 32 + (g16 & 1) * 16;
-        const v4 dlo = tile_read_tr<D, v4>(dl, rbase, dgrp, i16);
-        const v4 dhi = tile_read_tr<D, v4>(dl, rbase + 8, dgrp, i16);
-        const v4 qlo = tile_read_tr<D, v4>(ql, rbase, dgrp, i16);
-        const v4 qhi = tile_read_tr<D, v4>(ql, rbase + 8, dgrp, i16);
+        const v4 dlo = tile_read_tr<D, v4>(td, 0, ks, 0, db);
+        const v4 dhi = tile_read_tr<D, v4>(td, 0, ks, 1, db);
+        const v4 qlo = tile_read_tr<D, v4>(tq, 0, ks, 0, db);
+        const v4 qhi = tile_read_tr<D, v4>(tq, 0, ks, 1, db);
         dv[db] = mfma32(pa[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7), dv[db]);
         dk[db] = mfma32(sa[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7), dk[db]);
       }
@@ -253,8 +262,9 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   constexpr int TILE_BYTES = BN * D * 2;
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * TILE_BYTES];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hh = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hh = lane >> 5;
   const int N = p.N;
   const int nqb = (N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -262,6 +272,9 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const int qb = nqb - 1 - (L % nqb);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h / (p.Hq / p.Hkv);
   const uint32_t lds0 = lds_addr(smem);
+  const RowBase<D> rb(l32, hh);
+  const TrBase<D> tb(lane);
+  const LoadLane llk(lane, wave, p.k.ss), llv(lane, wave, p.v.ss);
 
   const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + h * p.q.sh;
   const T* dog = static_cast<const T*>(p.dout.ptr) + b * p.dout.sb + h * p.dout.sh;
@@ -278,8 +291,8 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const int ntiles = (kv_end + BN - 1) / BN;
   const int nfull = CAUSAL ? min(q0 / BN, N / BN) : N / BN;
 
-  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, lane);
-  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, lane);
+  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, llk);
+  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, llv);
 
   v8 qf[ND16], dof[ND16];
 #pragma unroll
@@ -303,9 +316,17 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
     const uint32_t vl = kl + TILE_BYTES;
     if (t + 1 < ntiles) {
       const uint32_t nk = lds0 + ((t + 1) & 1) * 2 * TILE_BYTES;
-      tile_load_async<D, BN, 4>(kg, p.k.ss, (t + 1) * BN, N, nk, wave, lane);
-      tile_load_async<D, BN, 4>(vg, p.v.ss, (t + 1) * BN, N, nk + TILE_BYTES, wave, lane);
+      const int r1 = (t + 1) * BN;
+      if (r1 + BN <= N) {
+        tile_load_pieces<D, BN, 4, false>(kg, p.k.ss, r1, N, nk, wave, llk);
+        tile_load_pieces<D, BN, 4, false>(vg, p.v.ss, r1, N, nk + TILE_BYTES, wave, llv);
+      } else {
+        tile_load_pieces<D, BN, 4, true>(kg, p.k.ss, r1, N, nk, wave, llk);
+        tile_load_pieces<D, BN, 4, true>(vg, p.v.ss, r1, N, nk + TILE_BYTES, wave, llv);
+      }
     }
+    const RowBase<D> rk = at_tile(rb, kl), rv = at_tile(rb, vl);
+    const TrBase<D> tk = at_tile(tb, kl);
     const int kbase = t * BN;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -314,8 +335,8 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int ds = 0; ds < ND16; ++ds) {
-        const v8 ka = tile_read16<D, v8>(kl, kb * 32 + l32, 2 * ds + hh);
-        const v8 va = tile_read16<D, v8>(vl, kb * 32 + l32, 2 * ds + hh);
+        const v8 ka = tile_read_row<D, v8>(rk, kb, ds);
+        const v8 va = tile_read_row<D, v8>(rv, kb, ds);
         s = mfma32(ka, qf[ds], s);
         dp = mfma32(va, dof[ds], dp);
       }
@@ -336,12 +357,10 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const int rbase = kb * 32 + ks * 16 + 4 * hh;
 #pragma unroll
         for (int db = 0; db < ND32; ++db) {
-          const int dgrp = db * 32 + (g16 & 1) * 16;
-          const v4 lo = tile_read_tr<D, v4>(kl, rbase, dgrp, i16);
-          const v4 hi = tile_read_tr<D, v4>(kl, rbase + 8, dgrp, i16);
+          const v4 lo = tile_read_tr<D, v4>(tk, kb, ks, 0, db);
+          const v4 hi = tile_read_tr<D, v4>(tk, kb, ks, 1, db);
           dq[db] = mfma32(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), sb[ks], dq[db]);
         }
       }

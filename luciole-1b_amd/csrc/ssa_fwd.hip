@@ -37,7 +37,7 @@ struct FwdTile {
 
   // S^T for the 64 keys of the tile at `kl` (LDS byte address), blocks kb
   // that are not `active` are skipped.
-  __device__ static __forceinline__ void scores(uint32_t kl, const v8* qf, int l32, int hh, const bool* active,
+  __device__ static __forceinline__ void scores(const RowBase<D>& rb, const v8* qf, const bool* active,
                                                 f32x16* s) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -45,26 +45,23 @@ struct FwdTile {
       if (!active[kb]) continue;
 #pragma unroll
       for (int ds = 0; ds < ND16; ++ds) {
-        const v8 a = tile_read16<D, v8>(kl, kb * 32 + l32, 2 * ds + hh);
+        const v8 a = tile_read_row<D, v8>(rb, kb, ds);
         s[kb] = mfma32(a, qf[ds], s[kb]);
       }
     }
   }
 
-  __device__ static __forceinline__ void pv(uint32_t vl, const v8 (*pb)[2], int lane, int hh, const bool* active,
+  __device__ static __forceinline__ void pv(const TrBase<D>& tb, const v8 (*pb)[2], const bool* active,
                                             f32x16* acc) {
-    const int g = lane >> 4, i = lane & 15;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       if (!active[kb]) continue;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const int rbase = kb * 32 + ks * 16 + 4 * hh;
 #pragma unroll
         for (int db = 0; db < ND32; ++db) {
-          const int dgrp = db * 32 + (g & 1) * 16;
-          const v4 lo = tile_read_tr<D, v4>(vl, rbase, dgrp, i);
-          const v4 hi = tile_read_tr<D, v4>(vl, rbase + 8, dgrp, i);
+          const v4 lo = tile_read_tr<D, v4>(tb, kb, ks, 0, db);
+          const v4 hi = tile_read_tr<D, v4>(tb, kb, ks, 1, db);
           const v8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           acc[db] = mfma32(va, pb[kb][ks], acc[db]);
         }
@@ -82,10 +79,13 @@ __device__ __forceinline__ void fwd_body(const FwdParams& p, const int N, const 
   constexpr int TILE_BYTES = BN * D * 2;
   constexpr int ND16 = D / 16, ND32 = D / 32;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const uint32_t lds0 = static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)(smem)));
+  const uint32_t lds0 = lds_addr(smem);
+  const RowBase<D> rb(l32, hh);
+  const TrBase<D> tb(lane);
+  const LoadLane llk(lane, wave, p.k.ss), llv(lane, wave, p.v.ss);
   // buffer t: K at lds0 + t*2*TILE_BYTES, V right after
   const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + h * p.q.sh;
   const char* kg = static_cast<const char*>(p.k.ptr) + (b * p.k.sb + hk * p.k.sh) * 2;
@@ -103,8 +103,8 @@ __device__ __forceinline__ void fwd_body(const FwdParams& p, const int N, const 
   // first tile that needs masks: the causal diagonal or the sequence end
   const int nfull = CAUSAL ? min(q0 / BN, N / BN) : N / BN;
 
-  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, lane);
-  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, lane);
+  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, llk);
+  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, llv);
 
   v8 qf[ND16];
 #pragma unroll
@@ -124,8 +124,14 @@ __device__ __forceinline__ void fwd_body(const FwdParams& p, const int N, const 
     const uint32_t vl = kl + TILE_BYTES;
     if (t + 1 < ntiles) {
       const uint32_t nk = lds0 + ((t + 1) & 1) * 2 * TILE_BYTES;
-      tile_load_async<D, BN, 4>(kg, p.k.ss, (t + 1) * BN, N, nk, wave, lane);
-      tile_load_async<D, BN, 4>(vg, p.v.ss, (t + 1) * BN, N, nk + TILE_BYTES, wave, lane);
+      const int r1 = (t + 1) * BN;
+      if (r1 + BN <= N) {
+        tile_load_pieces<D, BN, 4, false>(kg, p.k.ss, r1, N, nk, wave, llk);
+        tile_load_pieces<D, BN, 4, false>(vg, p.v.ss, r1, N, nk + TILE_BYTES, wave, llv);
+      } else {
+        tile_load_pieces<D, BN, 4, true>(kg, p.k.ss, r1, N, nk, wave, llk);
+        tile_load_pieces<D, BN, 4, true>(vg, p.v.ss, r1, N, nk + TILE_BYTES, wave, llv);
+      }
     }
     const int kbase = t * BN;
     bool active[2];
@@ -135,7 +141,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& p, const int N, const 
       active[kb] = !MASKED || (kstart < N && (!CAUSAL || kstart <= wq0 + 31));
     }
     f32x16 s[2];
-    FT::scores(kl, qf, l32, hh, active, s);
+    FT::scores(at_tile(rb, kl), qf, active, s);
 
     // Row extreme of the raw scores over valid keys (max for n >= 0, min for n < 0).
     float z = -INFINITY;
@@ -180,7 +186,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& p, const int N, const 
         pb[kb][r >> 3][r & 7] = static_cast<T>(pv);
       }
     }
-    FT::pv(vl, pb, lane, hh, active, acc);
+    FT::pv(at_tile(tb, vl), pb, active, acc);
   };
   for (int t = 0; t < nfull; ++t) tile(t, std::false_type{});
   for (int t = nfull; t < ntiles; ++t) tile(t, std::true_type{});

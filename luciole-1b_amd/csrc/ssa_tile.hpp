@@ -1,25 +1,26 @@
 // LDS tile staging shared by the kernels that stream K/V (or Q/dO) tiles.
 //
-// A tile is ROWS rows of D bf16/fp16 elements, row-major, 2*D bytes per row,
-// with no padding.  Bank conflicts are avoided by permuting the 16-byte chunks
-// of each row: logical chunk c of row r lives in slot c ^ swz(r).  With RP
-// rows per 256-byte bank window (RP = 256 / (2 D)),
-//   swz(r) = (((r / RP) % 4) << 2 | (r / 4) % 4) & (chunks per row - 1)
-// is a bijection on the slots of a row such that
-//   * 16 consecutive rows read at one logical chunk (ds_read_b128 operand
-//     fetches, one row per lane, 16 lanes per LDS cycle) hit 16 distinct
-//     16-byte bank groups, and
-//   * 4 aligned consecutive rows read at 4 aligned chunks (the 32 lanes of a
-//     ds_read_b64_tr_b16 transpose read that the LDS serves together) hit
-//     disjoint 64-byte bank groups.
-// Measured on MI355X: ~215 B/clk/CU for the b128 pattern and ~150 B/clk/CU
-// for the transpose pattern, the same as fully contiguous reads; plain rows
-// give 16 and 61 B/clk/CU, and no row padding is conflict-free for both.
+// Layout.  A tile is a stack of 32-row blocks of D bf16/fp16 columns.  Inside
+// a block the 16-byte chunks are stored chunk-major: chunk c (columns 8c..8c+7)
+// of all 32 rows occupies 512 contiguous bytes, and row r sits at position
+//   pos(r, c) = r ^ (4 * (c & 3))
+// in it.  So
+//   off(r, c) = (r / 32) * BLOCK + c * 512 + ((r % 32) ^ 4 (c & 3)) * 16.
+// MFMA operand fetches then hit no LDS bank conflicts:
+//   * ds_read_b128 of one chunk for 16 consecutive rows (one row per lane, 16
+//     lanes per LDS cycle) reads 256 contiguous bytes;
+//   * a ds_read_b64_tr_b16 transpose read (32 lanes per LDS cycle) takes 4
+//     aligned rows from 4 aligned chunks, whose positions differ in bits 2-3
+//     and so fall in 4 disjoint 64-byte bank groups,
+// and every operand address is one of two per-lane base offsets plus a
+// compile-time immediate (the row XOR depends only on the lane and on one bit
+// of the step index), which keeps address arithmetic out of the inner loops.
 //
-// Tiles are filled with global_load_lds_dwordx4: each instruction moves 1 KB,
-// lane L writing LDS bytes [16 L, 16 L + 16) of that KB, so the swizzle is
-// applied on the global side (which chunk each lane fetches).  Rows past the
-// end of the sequence are clamped to the last valid row; callers mask them.
+// Tiles are filled with global_load_lds_dwordx4: each instruction moves 1 KB
+// (two chunk columns of one block), lane L writing LDS bytes [16 L, 16 L + 16)
+// of that KB; the layout is applied on the global side (which 16 bytes each
+// lane fetches).  Rows past the end of the sequence are clamped to the last
+// valid row; callers mask them.
 #pragma once
 
 #include "ssa_common.hpp"
@@ -27,58 +28,150 @@
 namespace ssa {
 
 template <int D>
-struct TileLayout {
-  static constexpr int CPR = D / 8;               // 16-byte chunks per row
-  static constexpr int ROW_BYTES = D * 2;
-  static constexpr int RPI = 1024 / ROW_BYTES;    // rows per 1 KB load instruction
-  static constexpr int RP = 256 / ROW_BYTES;      // rows per 256-byte bank window
-  __device__ static __forceinline__ int swz(int r) {
-    return ((((r / RP) & 3) << 2) | ((r >> 2) & 3)) & (CPR - 1);
+struct BlockLayout {
+  static constexpr int CPR = D / 8;          // 16-byte chunks per row
+  static constexpr int BLOCK = 32 * D * 2;   // bytes per 32-row block
+  static constexpr int IPB = BLOCK / 1024;   // 1 KB load instructions per block
+};
+
+// Per-lane constants of the direct loads issued by one wave.  Wave w issues
+// the 1 KB pieces j = w, w + NW, ... of a tile; piece j covers chunks
+// c = 2 (j % IPB) + half (half = lane / 32) of block j / IPB.  With NW and IPB
+// even, c & 3 = 2 (w & 1) + half for all of them, so the row a lane fetches
+// inside a block, pos ^ 4 (c & 3), is fixed per lane.  Row strides below
+// 2^24 elements (checked on the host) keep every offset under 2^31.
+struct LoadLane {
+  uint32_t off;   // r * row stride + half * 16, bytes
+  uint32_t hoff;  // half * 16, bytes
+  int r;          // row within the block
+  __device__ __forceinline__ LoadLane(int lane, int wave, int64_t ss) {
+    const int pos = lane & 31, half = lane >> 5;
+    r = pos ^ (4 * (2 * (wave & 1) + half));
+    hoff = static_cast<uint32_t>(half * 16);
+    off = static_cast<uint32_t>(r * ss * 2) + hoff;
   }
-  // Byte offset of logical chunk c of row r.
-  __device__ static __forceinline__ int chunk_off(int r, int c) { return r * ROW_BYTES + ((c ^ swz(r)) << 4); }
 };
 
 // Issue the loads of one ROWS x D tile (rows row0.. of a [*, D] matrix with
 // row stride `ss` elements) into `lds` (byte address).  Called by all NW waves
-// of the workgroup; wave w issues instructions w, w + NW, ... (a wave may
-// issue none when the tile has fewer 1 KB pieces than there are waves).
-template <int D, int ROWS, int NW>
-__device__ __forceinline__ void tile_load_async(const void* gbase, int64_t ss, int row0, int nrows, uint32_t lds,
-                                                int wave, int lane) {
-  using TL = TileLayout<D>;
-  constexpr int NINST = ROWS * TL::ROW_BYTES / 1024;
-  static_assert(NINST * 1024 == ROWS * TL::ROW_BYTES, "tile must be a whole number of 1 KB pieces");
-  const int rl = lane / TL::CPR, slot = lane % TL::CPR;
+// of the workgroup with `wave` wave-uniform (an SGPR); a wave may issue none
+// when the tile has fewer 1 KB pieces than there are waves.  Rows at or past
+// `nrows` are clamped to nrows - 1.
+template <int D, int ROWS, int NW, bool CLAMP>
+__device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
+                                                 const LoadLane& ll) {
+  using BL = BlockLayout<D>;
+  constexpr int NINST = ROWS / 32 * BL::IPB;
+  constexpr int PER = (NINST + NW - 1) / NW;
 #pragma unroll
-  for (int j = wave; j < NINST; j += NW) {
-    const int r = j * TL::RPI + rl;
-    int grow = row0 + r;
-    grow = grow < nrows ? grow : nrows - 1;
-    const int c = slot ^ TL::swz(r);
-    const char* src = static_cast<const char*>(gbase) + (static_cast<int64_t>(grow) * ss + c * 8) * 2;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                     (__attribute__((address_space(3))) void*)(uintptr_t)(lds + j * 1024), 16, 0, 0);
+  for (int i = 0; i < PER; ++i) {
+    const int j = wave + NW * i;
+    if (NINST % NW != 0 && j >= NINST) break;
+    const int blk = j / BL::IPB, cp = j % BL::IPB;
+    if (!CLAMP) {
+      // buffer_load ... lds: descriptor base at row0 (scalar), per-lane row
+      // offset in a VGPR fixed for the kernel, block/chunk offset in soffset.
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(g + static_cast<int64_t>(row0) * ss * 2), static_cast<short>(0), 0x7fffffff, 0x00020000);
+      const int soff = static_cast<int>(blk * 32 * ss * 2 + cp * 32);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(uintptr_t)(lds + j * 1024),
+                                               16, ll.off, soff, 0, 0);
+    } else {
+      int grow = row0 + blk * 32 + ll.r;
+      grow = grow < nrows ? grow : nrows - 1;
+      const char* src = g + (static_cast<int64_t>(grow) * ss + cp * 16) * 2 + ll.hoff;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
+                                       (__attribute__((address_space(3))) void*)(uintptr_t)(lds + j * 1024), 16, 0, 0);
+    }
   }
 }
 
-// 16-byte fetch of logical chunk c of row r (an MFMA operand: 8 consecutive elements).
-template <int D, typename V>
-__device__ __forceinline__ V tile_read16(uint32_t lds, int r, int c) {
-  return *(const __attribute__((address_space(3))) V*)(uintptr_t)(lds + TileLayout<D>::chunk_off(r, c));
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void tile_load_async(const void* gbase, int64_t ss, int row0, int nrows, uint32_t lds,
+                                                int wave, const LoadLane& ll) {
+  static_assert(NW % 2 == 0 && BlockLayout<D>::IPB % 2 == 0, "chunk parity must be fixed per wave");
+  const char* g = static_cast<const char*>(gbase);
+  if (row0 + ROWS <= nrows)
+    tile_load_pieces<D, ROWS, NW, false>(g, ss, row0, nrows, lds, wave, ll);
+  else
+    tile_load_pieces<D, ROWS, NW, true>(g, ss, row0, nrows, lds, wave, ll);
 }
 
-// Transposed fetch for an MFMA operand that needs column d of rows rbase..rbase+3:
-// within each 16-lane group, lane i supplies row rbase + i/4, columns
-// dgrp + 4 (i%4) .. +3 (8 bytes), and receives column dgrp + i of the 4 rows.
-// dgrp = 16-column group of this lane's 16-lane group.
+// A VGPR copy of x that the compiler cannot re-associate with later
+// arithmetic: per-tile base addresses stay in registers and the operand
+// fetches use their immediate offset fields.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Per-lane base offsets for the row-wise operand fetch "row 32*blk + l32,
+// chunk 2*ds + hh": index by the parity of ds.
+template <int D>
+struct RowBase {
+  uint32_t b[2];
+  __device__ __forceinline__ RowBase(int l32, int hh) {
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int c = 2 * par + hh;  // c & 3 for chunk 2*ds + hh with ds & 1 == par
+      b[par] = static_cast<uint32_t>(hh * 512 + ((l32 ^ (4 * c)) << 4));
+    }
+  }
+};
+
+// The same bases moved to a tile at LDS byte address `lds`.
+template <int D>
+__device__ __forceinline__ RowBase<D> at_tile(const RowBase<D>& rb, uint32_t lds) {
+  RowBase<D> r = rb;
+  r.b[0] = opaque(rb.b[0] + lds);
+  r.b[1] = opaque(rb.b[1] + lds);
+  return r;
+}
+
+// 16-byte fetch of chunk 2*ds + hh of row 32*blk + l32 (an MFMA operand of 8
+// consecutive elements) of the tile whose bases are `rb` (see at_tile).  ds
+// and blk are compile-time at the call sites.
+template <int D, typename V>
+__device__ __forceinline__ V tile_read_row(const RowBase<D>& rb, int blk, int ds) {
+  const uint32_t imm = blk * BlockLayout<D>::BLOCK + ds * 2 * 512;
+  return *(const __attribute__((address_space(3))) V*)(uintptr_t)(rb.b[ds & 1] + imm);
+}
+
+// Per-lane base offsets for transpose fetches: within each 16-lane group g,
+// lane i supplies row rbase + i/4 (rbase = 16 ks + 8 hi + 4 hh inside a block)
+// and the 8 bytes at columns dgrp + 4 (i%4) with dgrp = 32 db + 16 (g&1);
+// indexed by hi.
+template <int D>
+struct TrBase {
+  uint32_t b[2];
+  __device__ __forceinline__ TrBase(int lane) {
+    const int g = lane >> 4, i = lane & 15, hh = lane >> 5;
+    const int cl = (g & 1) * 2 + ((i & 3) >> 1);  // chunk within the 32-column group (= c & 3)
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const int rl = 8 * hi + 4 * hh + (i >> 2);
+      b[hi] = static_cast<uint32_t>(cl * 512 + ((rl ^ (4 * cl)) << 4) + ((i & 1) << 3));
+    }
+  }
+};
+
+template <int D>
+__device__ __forceinline__ TrBase<D> at_tile(const TrBase<D>& tb, uint32_t lds) {
+  TrBase<D> r = tb;
+  r.b[0] = opaque(tb.b[0] + lds);
+  r.b[1] = opaque(tb.b[1] + lds);
+  return r;
+}
+
+// Transposed fetch: column 32*db + l32 of rows 32*blk + 16*ks + 8*hi + 4*hh + (0..3)
+// of the tile whose bases are `tb`, as 4 elements (k-slots 4*hi .. 4*hi+3 of
+// an MFMA operand whose contraction index runs over the rows).
 template <int D, typename V4>
-__device__ __forceinline__ V4 tile_read_tr(uint32_t lds, int rbase, int dgrp, int i) {
-  const int r = rbase + (i >> 2);
-  const int col = dgrp + 4 * (i & 3);
-  const uint32_t off = TileLayout<D>::chunk_off(r, col >> 3) + ((col & 4) << 1);
+__device__ __forceinline__ V4 tile_read_tr(const TrBase<D>& tb, int blk, int ks, int hi, int db) {
+  const uint32_t imm = blk * BlockLayout<D>::BLOCK + db * 4 * 512 + ks * 16 * 16;
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-  const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(lds + off));
+  const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(tb.b[hi] + imm));
   return __builtin_bit_cast(V4, v);
 }
 

@@ -86,6 +86,8 @@ def _bwd_args(**kw):
         ("ssa_n", None, _lib.SSA_ERR_NULL_POINTER),
         ("q", _lib.Tensor4(FAKE + 2, 0, 0, 128), _lib.SSA_ERR_ALIGNMENT),
         ("k", _lib.Tensor4(FAKE, 0, 0, 100), _lib.SSA_ERR_ALIGNMENT),
+        ("k", _lib.Tensor4(FAKE, 0, 0, 1 << 24), _lib.SSA_ERR_ALIGNMENT),
+        ("v", _lib.Tensor4(FAKE, -128, 0, 128), _lib.SSA_ERR_ALIGNMENT),
         ("v", _lib.Tensor4(None, 0, 0, 128), _lib.SSA_ERR_NULL_POINTER),
     ],
 )
