@@ -18,8 +18,9 @@
  *    memory on the host (n and b are read by the kernels through pointers).
  *  - Tensors are [batch, heads, seqlen, head_dim] views described by a base
  *    pointer and element strides for the first three dimensions; the last
- *    (head_dim) stride must be 1.  Base pointers must be 16-byte aligned and
- *    the three strides multiples of 8 elements.
+ *    (head_dim) stride must be 1.  Base pointers must be 16-byte aligned, the
+ *    three strides non-negative multiples of 8 elements, and the row
+ *    (seqlen) stride below 2^24 elements.
  *  - Results are bitwise deterministic run to run: no floating-point atomics,
  *    fixed-order reductions only.
  */
