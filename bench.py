@@ -52,6 +52,28 @@ CONFIGS = {
 }
 
 METRIC = "SSA attn fwd+bwd TFLOP/s and % bf16 MFMA peak, 1 MI355X, S=4096 D=128"
+COPY_MIB = 1024  # calibration copy of the --pmc-pass runs
+TRAFFIC_ROW = re.compile(r"^\|\s*`?(ssa_\w+?)`?\s*\|\s*([0-9.]+)\s*\|\s*([0-9.]+)\s*\|\s*([0-9.]+)\s*\|")
+
+
+def measured_traffic(config):
+    """HBM bytes per launch per kernel from the committed counter summary of this config.
+
+    profiles/hbm_traffic_<config>.md holds one table row per kernel:
+    | kernel | fetch MB | write MB | total MB | ... -- FETCH_SIZE and WRITE_SIZE per
+    dispatch from two rocprofv3 --pmc runs of `bench.py --pmc-pass`, each scaled by
+    the factor that makes the same counter read exactly the bytes of the
+    calibration copy.  Returns {} when the file is absent.
+    """
+    f = ROOT / "profiles" / f"hbm_traffic_{config}.md"
+    if not f.exists():
+        return {}
+    out = {}
+    for line in f.read_text().splitlines():
+        m = TRAFFIC_ROW.match(line)
+        if m:
+            out[m.group(1)] = float(m.group(4)) * 1e6
+    return out
 
 
 def pairs_dense(B, Hq, S, causal):
@@ -120,6 +142,9 @@ def main():
     ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="run each kernel of one step once, then a plain copy of COPY_MIB MiB "
+                         "(counter calibration), and exit; for rocprofv3 --pmc runs")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -153,6 +178,18 @@ def main():
     def step():
         out, m = ssa_flash_attn_forward(q, k, v, scale, n, bb, causal)
         return ssa_flash_attn_backward(q, k, v, out, do, m, scale, n, bb, causal)
+
+    if args.pmc_pass:
+        # One launch of every kernel, then the calibration copy: a device-to-device
+        # copy of COPY_MIB MiB reads and writes exactly that many bytes.
+        step()
+        torch.cuda.synchronize()
+        src = torch.empty(COPY_MIB << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] pmc pass done: one step + copy of {COPY_MIB} MiB")
+        return
 
     log(f"[bench] config={args.config} B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal} warmup={args.warmup}")
     for _ in range(args.warmup):
@@ -204,15 +241,18 @@ def main():
         if "alg_bytes" in kd:
             kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
             kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
+    traffic = measured_traffic(args.config) if args.dtype == "bf16" else {}
+    for name, kd in kernels.items():
+        kd["hbm_bytes"] = traffic.get(name)
     dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
     kd = kernels[dominant]
     if "tflops" in kd:
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": kd["tflops"] / PEAK_BF16_TFLOPS, "traffic": None,
+                    "unit": "TFLOP/s", "frac": kd["tflops"] / PEAK_BF16_TFLOPS, "traffic": kd["hbm_bytes"],
                     "avg_launch_ms": kd["avg_ms"]}
     else:
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": kd["gbps"], "peak": PEAK_HBM_GBPS,
-                    "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": None,
+                    "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": kd["hbm_bytes"],
                     "avg_launch_ms": kd["avg_ms"]}
 
     fwd_ms = kernels["ssa_fwd_kernel"]["avg_ms"]

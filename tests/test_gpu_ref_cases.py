@@ -22,7 +22,10 @@ from pathlib import Path
 import pytest
 import torch
 
-sys.path.insert(0, str(Path(__file__).resolve().parent))
+_HERE = Path(__file__).resolve().parent
+for _p in (_HERE, _HERE.parent, _HERE.parent / "luciole-1b_amd"):  # also when run as a script
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
 
 from test_gpu_parity import _check, _run  # noqa: E402
 
