@@ -99,9 +99,30 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const int nsub = (N - qstart + BMQ - 1) / BMQ;
   const int nsteps = G * nsub;
   const bool key_edge = k0 + BN > N;
+  // Step order: every sub-tile that needs masks first (the causal diagonal,
+  // a partial last sub-tile, or all of them at the sequence end), then the
+  // unmasked ones, so each of the two loops below has a single body.
+  const int nlo = key_edge ? nsub : (CAUSAL ? min(BN / BMQ, nsub) : 0);
+  const int ntail = (!key_edge && (N % BMQ) != 0 && nsub > nlo) ? 1 : 0;
+  const int per_m = nlo + ntail, per_u = nsub - per_m;  // per q-head
+  const int nmasked = G * per_m;
+  auto step_q0 = [&](int st, int& g) {
+    int i;
+    if (st < nmasked) {
+      g = st / per_m;
+      const int j = st - g * per_m;
+      i = j < nlo ? j : nsub - 1;
+    } else {
+      const int su = st - nmasked;
+      g = su / per_u;
+      i = nlo + (su - g * per_u);
+    }
+    return qstart + i * BMQ;
+  };
 
   auto issue = [&](int st, uint32_t buf) {
-    const int g = st / nsub, q0 = qstart + (st % nsub) * BMQ;
+    int g;
+    const int q0 = step_q0(st, g);
     const int hq = hk * G + g;
     const char* qg = static_cast<const char*>(p.q.ptr) + (b * p.q.sb + hq * p.q.sh) * 2;
     const char* dog = static_cast<const char*>(p.dout.ptr) + (b * p.dout.sb + hq * p.dout.sh) * 2;
@@ -195,20 +216,22 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     }
   };
 
-  for (int st = 0; st < nsteps; ++st) {
+  auto step = [&](int st, auto masked_tag) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const uint32_t buf = lds0 + (st & 1) * BUF;
     if (st + 1 < nsteps) issue(st + 1, lds0 + ((st + 1) & 1) * BUF);
-    const int q0 = qstart + (st % nsub) * BMQ;
-    if (k0w >= N) continue;
-    if (CAUSAL && q0 + BMQ - 1 < k0w) continue;
-    const bool masked = key_edge || q0 + BMQ > N || (CAUSAL && q0 < k0 + BN);
-    if (masked)
-      body(buf, q0, std::true_type{});
-    else
-      body(buf, q0, std::false_type{});
-  }
+    int g;
+    const int q0 = step_q0(st, g);
+    if (decltype(masked_tag)::value) {
+      if (k0w >= N) return;
+      if (CAUSAL && q0 + BMQ - 1 < k0w) return;
+    }
+    body(buf, q0, masked_tag);
+  };
+  int st = 0;
+  for (; st < nmasked; ++st) step(st, std::true_type{});
+  for (; st < nsteps; ++st) step(st, std::false_type{});
 
   // Store dK (scaled by scale * n * b) and dV: lane holds d = 32*db + l32,
   // key rows crow(r, hh) of this wave's 32 keys.
