@@ -63,6 +63,18 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 // Value of `x` in the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
 
+// max / sum of x over the lane pair (l, l ^ 32), in every lane: one
+// v_permlane32_swap (which leaves {x[l % 32], x[l % 32 + 32]} in its two
+// results in every lane) and one op, no LDS.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (block id % 8).  This
 // bijection on [0, total) gives each XCD a contiguous range of logical block
 // indices, so logical neighbours (same head) share one XCD's L2.

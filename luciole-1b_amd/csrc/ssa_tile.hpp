@@ -57,31 +57,67 @@ struct LoadLane {
 // of the workgroup with `wave` wave-uniform (an SGPR); a wave may issue none
 // when the tile has fewer 1 KB pieces than there are waves.  Rows at or past
 // `nrows` are clamped to nrows - 1.
+// Direct-to-LDS loads, written as inline assembly.  The compiler's wait-count
+// insertion, when it sees an LDS DMA builtin in flight, puts a full vmcnt(0)
+// wait in front of later LDS transpose reads, which would drain the tile
+// prefetch; issued from assembly the loads are invisible to it, and the
+// kernels order them explicitly (wait_vm<N>() + barrier before a tile is
+// read).  M0 holds the LDS destination (wave-uniform); one wait state is
+// required between writing M0 and the load.  No builtin that uses M0 is
+// compiled into these kernels.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor: base address, stride 0, no bounds check in practice.
+__device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{static_cast<int>(static_cast<uint32_t>(a)), static_cast<int>((a >> 32) & 0xffff), 0x7fffffff,
+                 0x00020000};
+}
+
+// 16 bytes per lane from rsrc.base + voff + soff to LDS [m0 + 16 lane].
+__device__ __forceinline__ void dma_buffer16(uint32_t lds, const i32x4_t& rsrc, uint32_t voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+// 16 bytes per lane from a per-lane global address to LDS [m0 + 16 lane].
+__device__ __forceinline__ void dma_global16(uint32_t lds, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(reinterpret_cast<uint64_t>(src))
+               : "memory", "m0");
+}
+
+// 4 bytes per lane from a per-lane global address to LDS [m0 + 4 lane].
+__device__ __forceinline__ void dma_global4(uint32_t lds, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(reinterpret_cast<uint64_t>(src))
+               : "memory", "m0");
+}
+
 template <int D, int ROWS, int NW, bool CLAMP>
 __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
                                                  const LoadLane& ll) {
   using BL = BlockLayout<D>;
   constexpr int NINST = ROWS / 32 * BL::IPB;
   constexpr int PER = (NINST + NW - 1) / NW;
+  const i32x4_t rs = raw_rsrc(g + static_cast<int64_t>(row0) * ss * 2);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int j = wave + NW * i;
     if (NINST % NW != 0 && j >= NINST) break;
     const int blk = j / BL::IPB, cp = j % BL::IPB;
     if (!CLAMP) {
-      // buffer_load ... lds: descriptor base at row0 (scalar), per-lane row
-      // offset in a VGPR fixed for the kernel, block/chunk offset in soffset.
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<char*>(g + static_cast<int64_t>(row0) * ss * 2), static_cast<short>(0), 0x7fffffff, 0x00020000);
-      const int soff = static_cast<int>(blk * 32 * ss * 2 + cp * 32);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(uintptr_t)(lds + j * 1024),
-                                               16, ll.off, soff, 0, 0);
+      // descriptor base at row0 (scalar), per-lane row offset fixed for the
+      // kernel (VGPR), block/chunk offset in soffset
+      dma_buffer16(lds + j * 1024, rs, ll.off, static_cast<int>(blk * 32 * ss * 2 + cp * 32));
     } else {
       int grow = row0 + blk * 32 + ll.r;
       grow = grow < nrows ? grow : nrows - 1;
-      const char* src = g + (static_cast<int64_t>(grow) * ss + cp * 16) * 2 + ll.hoff;
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                       (__attribute__((address_space(3))) void*)(uintptr_t)(lds + j * 1024), 16, 0, 0);
+      dma_global16(lds + j * 1024, g + (static_cast<int64_t>(grow) * ss + cp * 16) * 2 + ll.hoff);
     }
   }
 }
@@ -95,6 +131,15 @@ __device__ __forceinline__ void tile_load_async(const void* gbase, int64_t ss, i
     tile_load_pieces<D, ROWS, NW, false>(g, ss, row0, nrows, lds, wave, ll);
   else
     tile_load_pieces<D, ROWS, NW, true>(g, ss, row0, nrows, lds, wave, ll);
+}
+
+// Wait until at most N vector-memory instructions of this wave (direct tile
+// loads included) are outstanding.  gfx9 s_waitcnt: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima (no wait).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
 // A VGPR copy of x that the compiler cannot re-associate with later
@@ -175,6 +220,14 @@ __device__ __forceinline__ V4 tile_read_tr(const TrBase<D>& tb, int blk, int ks,
   return __builtin_bit_cast(V4, v);
 }
 
+// Wait until at most N LDS (and scalar-memory) operations of this wave are
+// outstanding; vmcnt and expcnt left at their maxima.
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (N << 8) | (3 << 14));
+}
+
 // 32 consecutive fp32 values of each of two vectors (rows row0.. of `a` and of
 // `b`, clamped to nrows - 1) into 256 bytes of LDS at `lds`: a first, then b.
 // One global_load_lds_dword issued by the calling wave.
@@ -183,8 +236,7 @@ __device__ __forceinline__ void pair32_load_async(const float* a, const float* b
   int r = row0 + (lane & 31);
   r = r < nrows ? r : nrows - 1;
   const float* src = (lane < 32 ? a : b) + r;
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                   (__attribute__((address_space(3))) void*)(uintptr_t)(lds), 4, 0, 0);
+  dma_global4(lds, src);
 }
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
