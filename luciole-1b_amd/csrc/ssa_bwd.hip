@@ -59,17 +59,27 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_kernel(BwdParams p) {
 // P^T and dS'^T come out of the accumulators already in A-operand order for
 // dV += P^T dO and dK += dS'^T Q; the B operands (dO, Q with the query index
 // as the contraction dimension) are LDS transpose reads of the same sub-tiles
-// the S and dP products read row-wise.  K and V stay in registers.  The
-// sub-tiles (Q, dO, M, Delta) are double-buffered in LDS by direct loads.
+// the S and dP products read row-wise.  K and V stay in registers, dK and dV
+// accumulate in AGPRs.
+//
+// Software pipeline, one slot per sub-tile: slot j issues the MFMAs of
+// dV/dK for sub-tile j - 1 and of S/dP for sub-tile j + 1, and the vector
+// work of sub-tile j (SSA transform, P, dS', dn/db sums).  The two streams are
+// independent inside a slot; in the steady state they are interleaved in 32
+// fenced ticks (one MFMA with its operand reads and a slice of a three-stage
+// element pipeline per tick), so the wave keeps the matrix unit busy while it
+// issues vector work.  Sub-tiles (Q, dO, M, Delta) live in four LDS buffers:
+// sub-tile t is loaded in slot t - 2 (its buffer last held t - 4, read for
+// the last time in slot t - 3) and complete at the start of slot t - 1.
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
-  constexpr int BN = 128, BMQ = 32;
+  constexpr int BN = 128, BMQ = 32, NB = 4;
   constexpr int ND16 = D / 16, ND32 = D / 32;
-  constexpr int TILE = BMQ * D * 2;   // one Q (or dO) sub-tile
+  constexpr int TILE = BMQ * D * 2;    // one Q (or dO) sub-tile
   constexpr int BUF = 2 * TILE + 256;  // Q, dO, M[32], Delta[32]
-  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
+  __shared__ __attribute__((aligned(1024))) char smem[NB * BUF];
   __shared__ float red[2][4];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -101,7 +111,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const bool key_edge = k0 + BN > N;
   // Step order: every sub-tile that needs masks first (the causal diagonal,
   // a partial last sub-tile, or all of them at the sequence end), then the
-  // unmasked ones, so each of the two loops below has a single body.
+  // unmasked ones.
   const int nlo = key_edge ? nsub : (CAUSAL ? min(BN / BMQ, nsub) : 0);
   const int ntail = (!key_edge && (N % BMQ) != 0 && nsub > nlo) ? 1 : 0;
   const int per_m = nlo + ntail, per_u = nsub - per_m;  // per q-head
@@ -119,11 +129,19 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     }
     return qstart + i * BMQ;
   };
+  // a masked step whose queries all precede this wave's keys (or no keys)
+  auto skipped = [&](int st) {
+    int g;
+    return st < nmasked && (k0w >= N || (CAUSAL && step_q0(st, g) + BMQ - 1 < k0w));
+  };
+  auto bufof = [&](int st) { return lds0 + (st & (NB - 1)) * BUF; };
 
-  auto issue = [&](int st, uint32_t buf) {
+  auto issue = [&](int st) {
+    if (st >= nsteps) return;
     int g;
     const int q0 = step_q0(st, g);
     const int hq = hk * G + g;
+    const uint32_t buf = bufof(st);
     const char* qg = static_cast<const char*>(p.q.ptr) + (b * p.q.sb + hq * p.q.sh) * 2;
     const char* dog = static_cast<const char*>(p.dout.ptr) + (b * p.dout.sb + hq * p.dout.sh) * 2;
     if (q0 + BMQ <= N) {
@@ -134,11 +152,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       tile_load_pieces<D, BMQ, 4, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
     }
     if (wave == 3) {
-      const int64_t rb = (static_cast<int64_t>(b) * p.Hq + hq) * N;
-      pair32_load_async(p.m + rb, p.delta + rb, q0, N, buf + 2 * TILE, lane);
+      const int64_t rw = (static_cast<int64_t>(b) * p.Hq + hq) * N;
+      pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
     }
   };
-  issue(0, lds0);
+  issue(0);
+  issue(1);
 
   v8 kf[ND16], vf[ND16];
 #pragma unroll
@@ -154,54 +173,31 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     dv[i] = f32x16{};
   }
   float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;
+  f32x16 sc, dc, sn, dn2;  // S, dP of sub-tiles j and j + 1
+  v8 pa[2], sa[2], pa2[2], sa2[2];  // P^T, dS'^T operands of sub-tiles j - 1 and j
 
-  auto body = [&](uint32_t buf, int q0, auto masked_tag) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    const uint32_t ml = buf + 2 * TILE;
-    const RowBase<D> rq = at_tile(rb, buf), rd = at_tile(rb, buf + TILE);
-    f32x16 s = f32x16{}, dp = f32x16{};
+  auto kahan = [&](float tdn, float tdb) {
+    const float y = tdn - dn_c, t = dn_acc + y;
+    dn_c = (t - dn_acc) - y;
+    dn_acc = t;
+    const float y2 = tdb - db_c, t2 = db_acc + y2;
+    db_c = (t2 - db_acc) - y2;
+    db_acc = t2;
+  };
+
+  // ---- generic pieces (masked steps, pipeline fill and drain) ----
+  auto sdp = [&](int st, f32x16& s_out, f32x16& d_out) {
+    const RowBase<D> rq = at_tile(rb, bufof(st)), rd = at_tile(rb, bufof(st) + TILE);
+    s_out = f32x16{};
+    d_out = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < ND16; ++ds) {
-      const v8 qa = tile_read_row<D, v8>(rq, 0, ds);
-      const v8 da = tile_read_row<D, v8>(rd, 0, ds);
-      s = mfma32(qa, kf[ds], s);
-      dp = mfma32(da, vf[ds], dp);
+      s_out = mfma32(tile_read_row<D, v8>(rq, 0, ds), kf[ds], s_out);
+      d_out = mfma32(tile_read_row<D, v8>(rd, 0, ds), vf[ds], d_out);
     }
-    v8 pa[2], sa[2];
-    float tdn = 0.f, tdb = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f32x4_t mv = lds_read_f4(ml + (8 * j + 4 * hh) * 4);
-      const f32x4_t dv4 = lds_read_f4(ml + 128 + (8 * j + 4 * hh) * 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * j + e;
-        const float x = s[r];
-        const float u1 = fmaf(c, fabsf(x), 1.f);
-        const float sl = copysignf(fast_log2(u1), x);
-        float pv = fast_exp2(fmaf(n, sl, -mv[e]));
-        if (MASKED) {
-          const int qi = q0 + crow(r, hh);
-          const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
-          pv = valid ? pv : 0.f;
-        }
-        const float dt = pv * (dp[r] - dv4[e]);
-        const float dsp = dt * fast_rcp(u1);
-        tdn = fmaf(dt, sl, tdn);
-        tdb = fmaf(dsp, x, tdb);
-        pa[r >> 3][r & 7] = static_cast<T>(pv);
-        sa[r >> 3][r & 7] = static_cast<T>(dsp);
-      }
-    }
-    {  // Kahan accumulation of the per-sub-tile sums
-      const float y = tdn - dn_c, t = dn_acc + y;
-      dn_c = (t - dn_acc) - y;
-      dn_acc = t;
-      const float y2 = tdb - db_c, t2 = db_acc + y2;
-      db_c = (t2 - db_acc) - y2;
-      db_acc = t2;
-    }
-    const TrBase<D> tq = at_tile(tb, buf), td = at_tile(tb, buf + TILE);
+  };
+  auto dvdk = [&](int st, const v8* pp, const v8* ss) {
+    const TrBase<D> tq = at_tile(tb, bufof(st)), td = at_tile(tb, bufof(st) + TILE);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -210,28 +206,193 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         const v4 dhi = tile_read_tr<D, v4>(td, 0, ks, 1, db);
         const v4 qlo = tile_read_tr<D, v4>(tq, 0, ks, 0, db);
         const v4 qhi = tile_read_tr<D, v4>(tq, 0, ks, 1, db);
-        dv[db] = mfma32(pa[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7), dv[db]);
-        dk[db] = mfma32(sa[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7), dk[db]);
+        dv[db] = mfma32(pp[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7), dv[db]);
+        dk[db] = mfma32(ss[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7), dk[db]);
       }
     }
   };
-
-  auto step = [&](int st, auto masked_tag) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    const uint32_t buf = lds0 + (st & 1) * BUF;
-    if (st + 1 < nsteps) issue(st + 1, lds0 + ((st + 1) & 1) * BUF);
+  auto elementwise = [&](int st, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     int g;
     const int q0 = step_q0(st, g);
-    if (decltype(masked_tag)::value) {
-      if (k0w >= N) return;
-      if (CAUSAL && q0 + BMQ - 1 < k0w) return;
+    const uint32_t ml = bufof(st) + 2 * TILE;
+    float tdn = 0.f, tdb = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4_t mv = lds_read_f4(ml + (8 * j + 4 * hh) * 4);
+      const f32x4_t dv4 = lds_read_f4(ml + 128 + (8 * j + 4 * hh) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * j + e;
+        const float x = sc[r];
+        const float u1 = fmaf(c, fabsf(x), 1.f);
+        const float sl = copysignf(fast_log2(u1), x);
+        float pv = fast_exp2(fmaf(n, sl, -mv[e]));
+        if (MASKED) {
+          const int qi = q0 + crow(r, hh);
+          const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
+          pv = valid ? pv : 0.f;
+        }
+        const float dt = pv * (dc[r] - dv4[e]);
+        const float dsp = dt * fast_rcp(u1);
+        tdn = fmaf(dt, sl, tdn);
+        tdb = fmaf(dsp, x, tdb);
+        pa2[r >> 3][r & 7] = static_cast<T>(pv);
+        sa2[r >> 3][r & 7] = static_cast<T>(dsp);
+      }
     }
-    body(buf, q0, masked_tag);
+    kahan(tdn, tdb);
   };
-  int st = 0;
-  for (; st < nmasked; ++st) step(st, std::true_type{});
-  for (; st < nsteps; ++st) step(st, std::false_type{});
+  auto rotate = [&]() {
+    sc = sn;
+    dc = dn2;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      pa[ks] = pa2[ks];
+      sa[ks] = sa2[ks];
+    }
+  };
+  auto slot_generic = [&](int j) {
+    wait_vm<0>();  // sub-tile j + 1
+    __builtin_amdgcn_s_barrier();
+    issue(j + 2);
+    if (j >= 1 && !skipped(j - 1)) dvdk(j - 1, pa, sa);
+    if (j + 1 < nsteps && !skipped(j + 1)) sdp(j + 1, sn, dn2);
+    if (j < nsteps && !skipped(j)) {
+      if (j < nmasked)
+        elementwise(j, std::true_type{});
+      else
+        elementwise(j, std::false_type{});
+    }
+    rotate();
+  };
+
+  // ---- steady-state slot: sub-tiles j - 1, j, j + 1 unmasked ----
+  auto slot_fast = [&](int j) {
+    constexpr int NG = 4 * ND32 + 2 * ND16;  // MFMAs per slot
+    constexpr int STRIDE = 32 / NG;           // ticks per MFMA
+    wait_vm<0>();  // sub-tile j + 1
+    __builtin_amdgcn_s_barrier();
+    issue(j + 2);
+    const TrBase<D> tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
+    const RowBase<D> rq = at_tile(rb, bufof(j + 1)), rd = at_tile(rb, bufof(j + 1) + TILE);
+    const uint32_t ml = bufof(j) + 2 * TILE;
+    f32x4_t mq[4], dq4[4];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      mq[g4] = lds_read_f4(ml + (8 * g4 + 4 * hh) * 4);
+      dq4[g4] = lds_read_f4(ml + 128 + (8 * g4 + 4 * hh) * 4);
+    }
+    v8 ops[3];
+    // MFMA g: g < 4 ND32 -> dV (even) / dK (odd) of sub-tile j - 1, pair (ks, db);
+    // else S (even) / dP (odd) of sub-tile j + 1, contraction slice ds.
+    auto read = [&](auto gc) {
+      constexpr int Gi = decltype(gc)::value;
+      if constexpr (Gi < 4 * ND32) {
+        constexpr int idx = Gi / 2, ks = idx / ND32, db = idx % ND32;
+        const TrBase<D>& t = (Gi % 2 == 0) ? td : tq;
+        const v4 lo = tile_read_tr<D, v4>(t, 0, ks, 0, db);
+        const v4 hi = tile_read_tr<D, v4>(t, 0, ks, 1, db);
+        ops[Gi % 3] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      } else if constexpr (Gi < NG) {
+        constexpr int h = Gi - 4 * ND32, ds = h / 2;
+        ops[Gi % 3] = tile_read_row<D, v8>((h % 2 == 0) ? rq : rd, 0, ds);
+      }
+    };
+    auto mfma = [&](auto gc) {
+      constexpr int Gi = decltype(gc)::value;
+      if constexpr (Gi < 4 * ND32) {
+        constexpr int idx = Gi / 2, ks = idx / ND32, db = idx % ND32;
+        if constexpr (Gi % 2 == 0)
+          dv[db] = mfma32(pa[ks], ops[Gi % 3], dv[db]);
+        else
+          dk[db] = mfma32(sa[ks], ops[Gi % 3], dk[db]);
+      } else {
+        constexpr int h = Gi - 4 * ND32, ds = h / 2;
+        if constexpr (h % 2 == 0)
+          sn = mfma32(ops[Gi % 3], kf[ds], ds == 0 ? f32x16{} : sn);
+        else
+          dn2 = mfma32(ops[Gi % 3], vf[ds], ds == 0 ? f32x16{} : dn2);
+      }
+    };
+    // element pipeline over the 16 entries of S_j / dP_j
+    //   A: u = 1 + c|x|, L = log2 u, 1/u
+    //   B: sL = copysign(L, x), p = exp2(n sL - M), dd = dP - Delta
+    //   C1: dT = p dd, dS' = dT / u      C2: dn, db sums, bf16 operands
+    // tick 2e: A(e + 2), C1(e); tick 2e + 1: B(e + 1), C2(e)
+    float Lv[16], rv[16], slv[16], pv[16], ddv[16], dtv[16], dsv[16];
+    float tdn = 0.f, tdb = 0.f;
+    auto A = [&](int e) {
+      const float x = sc[e];
+      const float u1 = fmaf(c, fabsf(x), 1.f);
+      Lv[e] = fast_log2(u1);
+      rv[e] = fast_rcp(u1);
+      pin(Lv[e]);
+      pin(rv[e]);
+    };
+    auto B = [&](int e) {
+      const float x = sc[e];
+      slv[e] = copysignf(Lv[e], x);
+      pv[e] = fast_exp2(fmaf(n, slv[e], -mq[e >> 2][e & 3]));
+      ddv[e] = dc[e] - dq4[e >> 2][e & 3];
+      pin(pv[e]);
+      pin(ddv[e]);
+    };
+    auto C1 = [&](int e) {
+      dtv[e] = pv[e] * ddv[e];
+      dsv[e] = dtv[e] * rv[e];
+      pin(dtv[e]);
+      pin(dsv[e]);
+    };
+    auto C2 = [&](int e) {
+      tdn = fmaf(dtv[e], slv[e], tdn);
+      tdb = fmaf(dsv[e], sc[e], tdb);
+      pin(tdn);
+      pin(tdb);
+      if (e & 1) {
+        pa2[e >> 3][(e & 7) - 1] = static_cast<T>(pv[e - 1]);
+        pa2[e >> 3][e & 7] = static_cast<T>(pv[e]);
+        sa2[e >> 3][(e & 7) - 1] = static_cast<T>(dsv[e - 1]);
+        sa2[e >> 3][e & 7] = static_cast<T>(dsv[e]);
+      }
+    };
+    auto tick = [&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      if constexpr (t % STRIDE == 0) {
+        read(std::integral_constant<int, t / STRIDE + 2>{});
+        mfma(std::integral_constant<int, t / STRIDE>{});
+      }
+      constexpr int e = t / 2;
+      if constexpr (t % 2 == 0) {
+        if constexpr (e + 2 < 16) A(e + 2);
+        C1(e);
+      } else {
+        if constexpr (e + 1 < 16) B(e + 1);
+        C2(e);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    read(std::integral_constant<int, 0>{});
+    read(std::integral_constant<int, 1>{});
+    A(0);
+    A(1);
+    B(0);
+    [&]<int... t>(std::integer_sequence<int, t...>) {
+      (tick(std::integral_constant<int, t>{}), ...);
+    }(std::make_integer_sequence<int, 32>{});
+    kahan(tdn, tdb);
+    rotate();
+  };
+
+  // prologue: sub-tiles 0 and 1 in flight, S/dP of sub-tile 0
+  wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  if (!skipped(0)) sdp(0, sn, dn2);
+  rotate();
+  int j = 0;
+  for (; j <= nmasked && j <= nsteps; ++j) slot_generic(j);
+  for (; j + 1 < nsteps; ++j) slot_fast(j);
+  for (; j <= nsteps; ++j) slot_generic(j);
 
   // Store dK (scaled by scale * n * b) and dV: lane holds d = 32*db + l32,
   // key rows crow(r, hh) of this wave's 32 keys.

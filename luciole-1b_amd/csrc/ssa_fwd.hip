@@ -71,10 +71,6 @@ struct FwdTile {
   }
 };
 
-// Value barrier: `x` is computed before this point (an empty side-effecting
-// statement the compiler must keep in order with scheduling fences).
-__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
-
 // ---------------------------------------------------------------------------
 // Software-pipelined forward.  One workgroup = 8 waves = 256 query rows (32
 // per wave), two waves per SIMD; K/V tiles of 64 keys in NB = 4 LDS buffers
