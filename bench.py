@@ -50,6 +50,20 @@ CONFIGS = {
     "s16384": (1, 16, 16, 16384, 128, True),
     "gqa_d64": (4, 32, 8, 4096, 64, True),   # production Luciole-1B attention shape
 }
+# packed sequences, 16384 tokens per micro-batch,
+# document lengths uniform in [64, 4096] from random.Random(1234), the last
+# document truncated to fill; H = 16, D = 128, causal inside each document.
+VARLEN_CONFIGS = {"varlen16k": (16384, 16, 16, 128, 64, 4096)}
+
+
+def varlen_lengths(total, lo, hi, seed=1234):
+    import random
+
+    rng = random.Random(seed)
+    lens = []
+    while sum(lens) < total:
+        lens.append(min(rng.randint(lo, hi), total - sum(lens)))
+    return lens
 
 METRIC = "SSA attn fwd+bwd TFLOP/s and % bf16 MFMA peak, 1 MI355X, S=4096 D=128"
 COPY_MIB = 1024  # calibration copy of the --pmc-pass runs
@@ -138,7 +152,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="s4096", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="s4096", choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS))
     ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
@@ -161,6 +175,8 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.config in VARLEN_CONFIGS:
+        return bench_varlen(args, dev)
     B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     torch.manual_seed(1234)
@@ -286,6 +302,67 @@ def main():
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(S, D, causal)
     print(json.dumps(result))
+
+
+def bench_varlen(args, dev):
+    """Packed-sequence fwd + bwd step; same JSON line."""
+    import torch
+
+    from SSA.ssa_hip_kernel import ssa_flash_attn_varlen_backward, ssa_flash_attn_varlen_forward
+
+    total, Hq, Hkv, D, lo, hi = VARLEN_CONFIGS[args.config]
+    lens = varlen_lengths(total, lo, hi)
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    torch.manual_seed(1234)
+    q = (torch.randn(total, Hq, D, device=dev) * 0.5).to(dtype)
+    k = (torch.randn(total, Hkv, D, device=dev) * 0.5).to(dtype)
+    v = (torch.randn(total, Hkv, D, device=dev) * 0.5).to(dtype)
+    do = torch.randn(total, Hq, D, device=dev).to(dtype)
+    cu = torch.tensor([0] + [sum(lens[: i + 1]) for i in range(len(lens))], dtype=torch.int32, device=dev)
+    n = torch.tensor(1.5, device=dev)
+    bb = torch.tensor(0.8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    maxlen = max(lens)
+    pairs = sum(Hq * L * (L + 1) // 2 for L in lens)
+    flops_fwd, flops_bwd = 4 * D * pairs, 10 * D * pairs
+
+    def fwd():
+        return ssa_flash_attn_varlen_forward(q, k, v, cu, maxlen, scale, n, bb, True)
+
+    def step():
+        out, m = fwd()
+        return ssa_flash_attn_varlen_backward(q, k, v, out, do, m, cu, maxlen, scale, n, bb, True)
+
+    log(f"[bench] config={args.config} docs={len(lens)} max={maxlen} pairs={pairs}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) / args.steps * 1e3
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.kernel_iters)]
+    for a, e in evs:
+        a.record(stream)
+        fwd()
+        e.record(stream)
+    torch.cuda.synchronize()
+    fwd_ms = sum(a.elapsed_time(e) for a, e in evs) / len(evs)
+    value = (flops_fwd + flops_bwd) / (ms_step * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "SSA attn fwd+bwd TFLOP/s, packed sequences (varlen), 1 MI355X",
+        "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: Q/K/V = 0.5 N(0,1), dO ~ N(0,1), seed 1234, n=1.5, b=0.8",
+        "config": {"workload": f"SSA attention varlen fwd+bwd ({args.config})", "total_tokens": total,
+                   "Hq": Hq, "Hkv": Hkv, "D": D, "causal": True, "documents": len(lens), "doc_lengths": lens,
+                   "pairs": pairs, "alg_gflop_per_step": (flops_fwd + flops_bwd) / 1e9},
+        "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
+        "fwd_ms": fwd_ms, "fwd_tflops": flops_fwd / (fwd_ms * 1e-3) / 1e12,
+    }))
 
 
 if __name__ == "__main__":

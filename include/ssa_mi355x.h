@@ -144,6 +144,38 @@ int32_t ssa_bwd_dkdv(const ssa_bwd_args* args, void* stream);
 int32_t ssa_bwd_dq(const ssa_bwd_args* args, void* stream);
 int32_t ssa_bwd_reduce(const ssa_bwd_args* args, void* stream);
 
+/*
+ * Packed (varlen) sequences.  q/k/v/out (and dout/dq/dk/dv) are token streams
+ * [total_tokens, heads, head_dim]: an ssa_tensor4 whose stride_b is ignored,
+ * stride_h is the head stride and stride_s the token stride.  cu_seqlens is a
+ * DEVICE array of batch + 1 int32 offsets (cu[0] = 0, nondecreasing,
+ * cu[batch] = total_tokens); document i = tokens [cu[i], cu[i+1]), and
+ * attention (causal or not) stays inside each document.  `seqlen` is the
+ * length of the longest document (max_seqlen).  m and delta are
+ * [heads_q, total_tokens] fp32; partials need
+ * ssa_bwd_partials_count(batch, heads_kv, seqlen) floats.  The table is read
+ * on the device only: entries are clamped to [0, total_tokens] and lengths to
+ * seqlen, so a malformed table gives wrong results but no out-of-bounds
+ * access.  No reference counterpart: the reference rejects packed sequences
+ * (training/train/train_ssa_triton/SSA/ssa_triton_attention.py:154-156); the
+ * layout is Megatron's PackedSeqParams (cu_seqlens_q, max_seqlen_q) as built
+ * by training/finetune/nemo_patch/data/packed_sequence.py:116-244.
+ */
+typedef struct {
+  ssa_fwd_args dense;          /* batch = documents, seqlen = max_seqlen */
+  const int32_t* cu_seqlens;   /* device, batch + 1 entries */
+  int32_t total_tokens;
+} ssa_varlen_fwd_args;
+
+typedef struct {
+  ssa_bwd_args dense;          /* batch = documents, seqlen = max_seqlen */
+  const int32_t* cu_seqlens;   /* device, batch + 1 entries */
+  int32_t total_tokens;
+} ssa_varlen_bwd_args;
+
+int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* args, void* stream);
+int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,10 +6,17 @@ Modules mirror the reference package ``training/train/train_ssa_triton/SSA``:
 layer names, re-exported from ``ssa_hip_kernel``).
 """
 
-from .ssa_flash_attention import SSAFlashAttnFunc, ssa_flash_attention  # noqa: F401
+from .ssa_flash_attention import (  # noqa: F401
+    SSAFlashAttnFunc,
+    SSAFlashAttnVarlenFunc,
+    ssa_flash_attention,
+    ssa_flash_attention_varlen,
+)
 from .ssa_hip_kernel import (  # noqa: F401
     ssa_bwd_preprocess,
     ssa_flash_attn_backward,
     ssa_flash_attn_forward,
+    ssa_flash_attn_varlen_backward,
+    ssa_flash_attn_varlen_forward,
     warmup_ssa_triton_kernels,
 )

@@ -37,6 +37,8 @@ EXPORTED_SYMBOLS = (
     "ssa_bwd_dkdv",
     "ssa_bwd_dq",
     "ssa_bwd_reduce",
+    "ssa_varlen_fwd",
+    "ssa_varlen_bwd",
 )
 
 ABI_VERSION = 1
@@ -99,6 +101,14 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+class VarlenFwdArgs(ctypes.Structure):
+    _fields_ = [("dense", FwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
+
+
+class VarlenBwdArgs(ctypes.Structure):
+    _fields_ = [("dense", BwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -112,6 +122,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssa_bwd_partials_count.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
     for name, argt in (("ssa_fwd", FwdArgs), ("ssa_bwd", BwdArgs), ("ssa_bwd_preprocess", BwdArgs),
                        ("ssa_bwd_dkdv", BwdArgs), ("ssa_bwd_dq", BwdArgs), ("ssa_bwd_reduce", BwdArgs)):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int32
+        fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
+    for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]

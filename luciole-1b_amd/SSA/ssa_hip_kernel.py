@@ -9,6 +9,10 @@ layer ``training/train/train_ssa_triton/SSA/ssa_triton_kernel.py``:
   -> (dq, dk, dv, dn, db)`` (reference :795-897)
 * ``warmup_ssa_triton_kernels(B, Hq, Hkv, N, D, dtype, device)`` (reference :904-928)
 
+plus packed-sequence (varlen) versions of the forward and backward, which the
+reference does not have (``ssa_flash_attn_varlen_forward`` /
+``ssa_flash_attn_varlen_backward``).
+
 Tensors are ``[B, H, N, D]`` with any strides whose last one is 1 (other
 layouts are made contiguous first); outputs follow the input strides
 (``torch.empty_like``).  ``m`` is the fp32 base-2 row normaliser
@@ -191,6 +195,109 @@ def ssa_bwd_preprocess(out, dout):
         _lib.check(_lib.lib().ssa_bwd_preprocess(ctypes.byref(args), ctypes.c_void_p(stream)),
                    "ssa_bwd_preprocess")
     return delta
+
+
+# ---------------------------------------------------------------------------
+# Packed (varlen) sequences: token streams [T, H, D] split into documents by
+# cu_seqlens, the layout of Megatron's PackedSeqParams (cu_seqlens_q,
+# max_seqlen_q; training/finetune/nemo_patch/data/packed_sequence.py:116-244).
+# The reference rejects packed sequences
+# (training/train/train_ssa_triton/SSA/ssa_triton_attention.py:154-156); here
+# attention (causal or not) stays inside each document.
+
+
+def _thd_layout(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` ([T, H, D]) or a contiguous copy that the kernels can address."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        return t.contiguous()
+    for dim in range(2):
+        if t.shape[dim] > 1 and t.stride(dim) % 8 != 0:
+            return t.contiguous()
+    if t.shape[0] > 1 and t.stride(0) >= _MAX_ROW_STRIDE:
+        return t.contiguous()
+    return t
+
+
+def _t3(t: torch.Tensor) -> _lib.Tensor4:
+    return _lib.Tensor4(t.data_ptr(), 0, t.stride(1) if t.shape[1] > 1 else 0, t.stride(0) if t.shape[0] > 1 else 0)
+
+
+def _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen):
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("packed q, k, v must be 3-D [total_tokens, H, D] tensors")
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    assert Hq % Hkv == 0, f"Hq={Hq} must be divisible by Hkv={Hkv}"
+    assert _is_pow2(D), f"Head dim D={D} must be a power of two"
+    if tuple(k.shape) != (T, Hkv, D) or tuple(v.shape) != (T, Hkv, D):
+        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share one dtype, bf16 or fp16")
+    if not (q.is_cuda and k.device == q.device and v.device == q.device):
+        raise ValueError("q, k, v must be on the same GPU device")
+    if not torch.is_tensor(cu_seqlens) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor of documents + 1 offsets")
+    cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    max_seqlen = int(max_seqlen)
+    return cu, cu.numel() - 1, T, Hq, Hkv, D, max_seqlen
+
+
+def ssa_flash_attn_varlen_forward(q, k, v, cu_seqlens, max_seqlen, softmax_scale, ssa_n, ssa_b, causal=True):
+    """Packed-sequence forward.  q [T,Hq,D], k/v [T,Hkv,D], cu_seqlens [docs+1]
+    (int32, on the device), max_seqlen = longest document.  Returns
+    ``(out [T,Hq,D], m [Hq,T] fp32)``."""
+    cu, docs, T, Hq, Hkv, D, max_seqlen = _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen)
+    q, k, v = _thd_layout(q), _thd_layout(k), _thd_layout(v)
+    n32 = _scalar(ssa_n, q.device)
+    b32 = _scalar(ssa_b, q.device)
+    out = _thd_layout(torch.empty_like(q))
+    m = torch.empty((Hq, T), device=q.device, dtype=torch.float32)
+    dense = _lib.FwdArgs(
+        _t3(q), _t3(k), _t3(v), _t3(out),
+        m.data_ptr(), n32.data_ptr(), b32.data_ptr(),
+        docs, Hq, Hkv, max_seqlen, D, _DTYPES[q.dtype], int(bool(causal)), float(softmax_scale),
+    )
+    args = _lib.VarlenFwdArgs(dense, cu.data_ptr(), T)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.check(_lib.lib().ssa_varlen_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_varlen_fwd")
+    return out, m
+
+
+def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen, softmax_scale, ssa_n, ssa_b,
+                                   causal=True):
+    """Packed-sequence backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors."""
+    cu, docs, T, Hq, Hkv, D, max_seqlen = _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen)
+    if tuple(out.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape) or out.dtype != q.dtype:
+        raise ValueError("out and dout must have the shape (and out the dtype) of q")
+    q, k, v = _thd_layout(q), _thd_layout(k), _thd_layout(v)
+    out, dout = _thd_layout(out), _thd_layout(dout.to(q.dtype))
+    m = m.to(torch.float32).contiguous()
+    if tuple(m.shape) != (Hq, T):
+        raise ValueError(f"m must be [Hq, T] = {(Hq, T)}, got {tuple(m.shape)}")
+    dev = q.device
+    n32 = _scalar(ssa_n, dev)
+    b32 = _scalar(ssa_b, dev)
+    dq = _thd_layout(torch.empty_like(q))
+    dk = _thd_layout(torch.empty_like(k))
+    dv = _thd_layout(torch.empty_like(v))
+    delta = torch.empty((Hq, T), device=dev, dtype=torch.float32)
+    lib = _lib.lib()
+    partials = torch.empty(max(int(lib.ssa_bwd_partials_count(docs, Hkv, max(max_seqlen, 1))), 1),
+                           device=dev, dtype=torch.float32)
+    dn = torch.empty((), device=dev, dtype=torch.float32)
+    db = torch.empty((), device=dev, dtype=torch.float32)
+    dense = _lib.BwdArgs(
+        _t3(q), _t3(k), _t3(v), _t3(out), _t3(dout), _t3(dq), _t3(dk), _t3(dv),
+        m.data_ptr(), delta.data_ptr(), partials.data_ptr(), dn.data_ptr(), db.data_ptr(),
+        n32.data_ptr(), b32.data_ptr(),
+        docs, Hq, Hkv, max_seqlen, D, _DTYPES[q.dtype], int(bool(causal)), float(softmax_scale),
+    )
+    args = _lib.VarlenBwdArgs(dense, cu.data_ptr(), T)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(lib.ssa_varlen_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_varlen_bwd")
+    return dq, dk, dv, dn, db
 
 
 def warmup_ssa_triton_kernels(

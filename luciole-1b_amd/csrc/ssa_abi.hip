@@ -80,6 +80,41 @@ int32_t fill_bwd(const ssa_bwd_args* a, ssa::BwdParams* p, bool preprocess_only)
   p->Hkv = a->heads_kv;
   p->N = a->seqlen;
   p->scale = a->softmax_scale;
+  p->cu_seqlens = nullptr;
+  p->T = 0;
+  return SSA_OK;
+}
+
+int32_t fill_fwd(const ssa_fwd_args* a, ssa::FwdParams* p) {
+  if (a == nullptr) return SSA_ERR_NULL_POINTER;
+  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
+  SSA_TRY(check_tensor(a->q, true));
+  SSA_TRY(check_tensor(a->k, true));
+  SSA_TRY(check_tensor(a->v, true));
+  SSA_TRY(check_tensor(a->out, true));
+  if (a->m == nullptr || a->ssa_n == nullptr || a->ssa_b == nullptr) return SSA_ERR_NULL_POINTER;
+  p->q = to_t4(a->q);
+  p->k = to_t4(a->k);
+  p->v = to_t4(a->v);
+  p->o = to_t4(a->out);
+  p->m = a->m;
+  p->n_ptr = a->ssa_n;
+  p->b_ptr = a->ssa_b;
+  p->B = a->batch;
+  p->Hq = a->heads_q;
+  p->Hkv = a->heads_kv;
+  p->N = a->seqlen;
+  p->scale = a->softmax_scale;
+  p->cu_seqlens = nullptr;
+  p->T = 0;
+  return SSA_OK;
+}
+
+// Packed batches: the document table itself lives on the device and is only
+// clamped there (see SeqView); the host checks what it can see.
+int32_t check_varlen(int32_t docs, int32_t max_seqlen, const int32_t* cu, int32_t total) {
+  if (cu == nullptr) return SSA_ERR_NULL_POINTER;
+  if (total <= 0 || docs <= 0 || max_seqlen <= 0 || max_seqlen > total) return SSA_ERR_CU_SEQLENS;
   return SSA_OK;
 }
 
@@ -102,7 +137,9 @@ const char* ssa_status_string(int32_t status) {
       return "unsupported tensor layout (base pointer 16-byte aligned, strides non-negative multiples of 8 "
              "elements, row stride below 2^24 elements)";
     case SSA_ERR_LAUNCH: return "HIP kernel launch failed";
-    case SSA_ERR_CU_SEQLENS: return "invalid cu_seqlens";
+    case SSA_ERR_CU_SEQLENS:
+      return "invalid packed-sequence arguments (total_tokens, documents and max_seqlen must be > 0, "
+             "max_seqlen <= total_tokens)";
     default: return "unknown status";
   }
 }
@@ -113,58 +150,73 @@ int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen) 
 }
 
 int32_t ssa_fwd(const ssa_fwd_args* a, void* stream) {
-  if (a == nullptr) return SSA_ERR_NULL_POINTER;
-  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
-  SSA_TRY(check_tensor(a->q, true));
-  SSA_TRY(check_tensor(a->k, true));
-  SSA_TRY(check_tensor(a->v, true));
-  SSA_TRY(check_tensor(a->out, true));
-  if (a->m == nullptr || a->ssa_n == nullptr || a->ssa_b == nullptr) return SSA_ERR_NULL_POINTER;
-  ssa::FwdParams p;
-  p.q = to_t4(a->q);
-  p.k = to_t4(a->k);
-  p.v = to_t4(a->v);
-  p.o = to_t4(a->out);
-  p.m = a->m;
-  p.n_ptr = a->ssa_n;
-  p.b_ptr = a->ssa_b;
-  p.B = a->batch;
-  p.Hq = a->heads_q;
-  p.Hkv = a->heads_kv;
-  p.N = a->seqlen;
-  p.scale = a->softmax_scale;
+  ssa::FwdParams p{};
+  SSA_TRY(fill_fwd(a, &p));
   return launch_status(
       ssa::launch_fwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
+int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* va, void* stream) {
+  if (va == nullptr) return SSA_ERR_NULL_POINTER;
+  const ssa_fwd_args* a = &va->dense;
+  ssa::FwdParams p{};
+  SSA_TRY(fill_fwd(a, &p));
+  SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
+  p.cu_seqlens = va->cu_seqlens;
+  p.T = va->total_tokens;
+  return launch_status(
+      ssa::launch_fwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
+}
+
+int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
+  if (va == nullptr) return SSA_ERR_NULL_POINTER;
+  const ssa_bwd_args* a = &va->dense;
+  ssa::BwdParams p{};
+  SSA_TRY(fill_bwd(a, &p, false));
+  SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
+  p.cu_seqlens = va->cu_seqlens;
+  p.T = va->total_tokens;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool causal = a->causal != 0;
+  // Delta over the whole token stream: one sequence of T rows, [H, T] layout.
+  ssa::BwdParams pre = p;
+  pre.cu_seqlens = nullptr;
+  pre.B = 1;
+  pre.N = va->total_tokens;
+  SSA_TRY(launch_status(ssa::launch_bwd_preprocess(pre, a->dtype, a->head_dim, s)));
+  SSA_TRY(launch_status(ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, causal, s)));
+  SSA_TRY(launch_status(ssa::launch_bwd_dq(p, a->dtype, a->head_dim, causal, s)));
+  return launch_status(ssa::launch_reduce_partials(p, s));
+}
+
 int32_t ssa_bwd_preprocess(const ssa_bwd_args* a, void* stream) {
-  ssa::BwdParams p;
+  ssa::BwdParams p{};
   SSA_TRY(fill_bwd(a, &p, true));
   return launch_status(ssa::launch_bwd_preprocess(p, a->dtype, a->head_dim, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_dkdv(const ssa_bwd_args* a, void* stream) {
-  ssa::BwdParams p;
+  ssa::BwdParams p{};
   SSA_TRY(fill_bwd(a, &p, false));
   return launch_status(
       ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_dq(const ssa_bwd_args* a, void* stream) {
-  ssa::BwdParams p;
+  ssa::BwdParams p{};
   SSA_TRY(fill_bwd(a, &p, false));
   return launch_status(
       ssa::launch_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_reduce(const ssa_bwd_args* a, void* stream) {
-  ssa::BwdParams p;
+  ssa::BwdParams p{};
   SSA_TRY(fill_bwd(a, &p, false));
   return launch_status(ssa::launch_reduce_partials(p, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd(const ssa_bwd_args* a, void* stream) {
-  ssa::BwdParams p;
+  ssa::BwdParams p{};
   SSA_TRY(fill_bwd(a, &p, false));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool causal = a->causal != 0;

@@ -85,13 +85,23 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int N = p.N;
-  const int nkb = dkdv_key_blocks(N);
+  const int nkb = dkdv_key_blocks(p.N);
   const int L = xcd_remap(blockIdx.x, gridDim.x);
+  // Logical order (kv-head, sequence, key block), as in the forward.
   const int bhk = L / nkb;
   const int kb = L % nkb;  // ascending = heaviest first under causal
-  const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
+  const int b = bhk % p.B, hk = bhk / p.B;
   const int G = p.Hq / p.Hkv;
+  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
+  const int N = sv.N;
+  if (kb * BN >= N) {  // packed: past the end of a shorter document
+    if (tid == 0) {
+      const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
+      p.partials[static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
+      p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
+    }
+    return;
+  }
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;
   const uint32_t lds0 = lds_addr(smem);
@@ -102,8 +112,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const int k0 = kb * BN;
   const int k0w = k0 + wave * 32;
   const int key = k0w + l32;
-  const T* kg = static_cast<const T*>(p.k.ptr) + b * p.k.sb + hk * p.k.sh;
-  const T* vg = static_cast<const T*>(p.v.ptr) + b * p.v.sb + hk * p.v.sh;
+  const T* kg = static_cast<const T*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
+  const T* vg = static_cast<const T*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
 
   const int qstart = CAUSAL ? k0 : 0;
   const int nsub = (N - qstart + BMQ - 1) / BMQ;
@@ -142,8 +152,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const int q0 = step_q0(st, g);
     const int hq = hk * G + g;
     const uint32_t buf = bufof(st);
-    const char* qg = static_cast<const char*>(p.q.ptr) + (b * p.q.sb + hq * p.q.sh) * 2;
-    const char* dog = static_cast<const char*>(p.dout.ptr) + (b * p.dout.sb + hq * p.dout.sh) * 2;
+    const char* qg = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + hq * p.q.sh) * 2;
+    const char* dog = static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + hq * p.dout.sh) * 2;
     if (q0 + BMQ <= N) {
       tile_load_pieces<D, BMQ, 4, false>(qg, p.q.ss, q0, N, buf, wave, llq);
       tile_load_pieces<D, BMQ, 4, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       tile_load_pieces<D, BMQ, 4, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
     }
     if (wave == 3) {
-      const int64_t rw = (static_cast<int64_t>(b) * p.Hq + hq) * N;
+      const int64_t rw = sv.mrow(b, hq, p.Hq, p.T, p.N);
       pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
     }
   };
@@ -397,8 +407,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // Store dK (scaled by scale * n * b) and dV: lane holds d = 32*db + l32,
   // key rows crow(r, hh) of this wave's 32 keys.
   const float kscale = p.scale * n * *p.b_ptr;
-  T* dkg = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + b * p.dk.sb + hk * p.dk.sh;
-  T* dvg = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + b * p.dv.sb + hk * p.dv.sh;
+  T* dkg = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;
+  T* dvg = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh;
 #pragma unroll
   for (int db = 0; db < ND32; ++db) {
 #pragma unroll
@@ -449,21 +459,24 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int N = p.N;
-  const int nqb = (N + BM - 1) / BM;
+  const int nqb = (p.N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = L / nqb;
+  // Logical order (head, sequence, query block), as in the forward.
+  const int hb = L / nqb;
   const int qb = nqb - 1 - (L % nqb);
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h / (p.Hq / p.Hkv);
+  const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
+  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
+  const int N = sv.N;
+  if (qb * BM >= N) return;  // packed: past the end of a shorter document
   const uint32_t lds0 = lds_addr(smem);
   const RowBase<D> rb(l32, hh);
   const TrBase<D> tb(lane);
   const LoadLane llk(lane, wave, p.k.ss), llv(lane, wave, p.v.ss);
 
-  const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + h * p.q.sh;
-  const T* dog = static_cast<const T*>(p.dout.ptr) + b * p.dout.sb + h * p.dout.sh;
-  const char* kg = static_cast<const char*>(p.k.ptr) + (b * p.k.sb + hk * p.k.sh) * 2;
-  const char* vg = static_cast<const char*>(p.v.ptr) + (b * p.v.sb + hk * p.v.sh) * 2;
+  const T* qg = static_cast<const T*>(p.q.ptr) + sv.off(p.q, b) + h * p.q.sh;
+  const T* dog = static_cast<const T*>(p.dout.ptr) + sv.off(p.dout, b) + h * p.dout.sh;
+  const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
+  const char* vg = static_cast<const char*>(p.v.ptr) + (sv.off(p.v, b) + hk * p.v.sh) * 2;
 
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;
@@ -484,7 +497,7 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
     qf[ds] = qrow < N ? load16<v8>(qg + qrow * p.q.ss + ds * 16 + 8 * hh) : zero8<v8>();
     dof[ds] = qrow < N ? load16<v8>(dog + qrow * p.dout.ss + ds * 16 + 8 * hh) : zero8<v8>();
   }
-  const int64_t rowbase = static_cast<int64_t>(bh) * N;
+  const int64_t rowbase = sv.mrow(b, h, p.Hq, p.T, p.N);
   const float mq = qrow < N ? p.m[rowbase + qrow] : 0.f;
   const float dlq = qrow < N ? p.delta[rowbase + qrow] : 0.f;
 
@@ -555,7 +568,7 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
 
   const float qscale = p.scale * n * *p.b_ptr;
   if (qrow < N) {
-    T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + b * p.dq.sb + h * p.dq.sh + qrow * p.dq.ss;
+    T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + qrow * p.dq.ss;
 #pragma unroll
     for (int db = 0; db < ND32; ++db) {
 #pragma unroll

@@ -94,6 +94,11 @@ struct Tensor4 {
   int64_t sb, sh, ss;
 };
 
+// Dense batches: B sequences of length N, sequence b at element offset
+// b * sb of each tensor, row-normaliser M / Delta of (b, h) at (b H + h) N.
+// Packed (varlen) batches: cu_seqlens != nullptr, B documents of a [T, H, D]
+// token stream, document b = tokens [cu[b], cu[b+1]) (N = the longest),
+// M / Delta laid out [H, T].
 struct FwdParams {
   Tensor4 q, k, v, o;
   float* m;
@@ -101,6 +106,8 @@ struct FwdParams {
   const float* b_ptr;
   int B, Hq, Hkv, N;
   float scale;
+  const int* cu_seqlens;
+  int T;
 };
 
 struct BwdParams {
@@ -114,6 +121,36 @@ struct BwdParams {
   const float* b_ptr;
   int B, Hq, Hkv, N;
   float scale;
+  const int* cu_seqlens;
+  int T;
+};
+
+// The sequence a workgroup works on.  For packed batches the document table
+// is clamped to [0, T] and the length to N, so any table keeps every access
+// inside the token stream.
+struct SeqView {
+  int N;         // length of this sequence
+  int64_t tok0;  // packed: first token of the document
+  bool packed;
+  __device__ __forceinline__ SeqView(const int* cu, int T, int Nmax, int b) {
+    packed = cu != nullptr;
+    if (packed) {
+      int s0 = cu[b], s1 = cu[b + 1];
+      s0 = s0 < 0 ? 0 : (s0 > T ? T : s0);
+      s1 = s1 < s0 ? s0 : (s1 > T ? T : s1);
+      tok0 = s0;
+      N = s1 - s0 < Nmax ? s1 - s0 : Nmax;
+    } else {
+      tok0 = 0;
+      N = Nmax;
+    }
+  }
+  // element offset of the sequence in a tensor (before the head offset)
+  __device__ __forceinline__ int64_t off(const Tensor4& t, int b) const { return packed ? tok0 * t.ss : b * t.sb; }
+  // index of row 0 of (b, h) in M / Delta
+  __device__ __forceinline__ int64_t mrow(int b, int h, int H, int T, int Nmax) const {
+    return packed ? static_cast<int64_t>(h) * T + tok0 : (static_cast<int64_t>(b) * H + h) * Nmax;
+  }
 };
 
 constexpr float kLn2 = 0.69314718055994530942f;

@@ -85,7 +85,7 @@ struct FwdTile {
 // iteration t - 2 (its buffer last held tile t - 4, whose V was last read in
 // iteration t - 3) and must be complete at the start of iteration t - 1.
 template <typename T, int D, bool CAUSAL, bool NPOS>
-__device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const int N, const int bh, const int qb, const int b,
+__device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& sv, const int qb, const int b,
                                             const int h, const int hk, char* smem) {
   typedef FwdTile<T, D> FT;
   typedef typename FT::v8 v8;
@@ -103,10 +103,11 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const int N, con
   const RowBase<D> rb(l32, hh);
   const TrBase<D> tb(lane);
   const LoadLane llk(lane, wave, p.k.ss), llv(lane, wave, p.v.ss);
-  const T* qg = static_cast<const T*>(p.q.ptr) + b * p.q.sb + h * p.q.sh;
-  const char* kg = static_cast<const char*>(p.k.ptr) + (b * p.k.sb + hk * p.k.sh) * 2;
-  const char* vg = static_cast<const char*>(p.v.ptr) + (b * p.v.sb + hk * p.v.sh) * 2;
-  T* og = static_cast<T*>(const_cast<void*>(p.o.ptr)) + b * p.o.sb + h * p.o.sh;
+  const int N = sv.N;
+  const T* qg = static_cast<const T*>(p.q.ptr) + sv.off(p.q, b) + h * p.q.sh;
+  const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
+  const char* vg = static_cast<const char*>(p.v.ptr) + (sv.off(p.v, b) + hk * p.v.sh) * 2;
+  T* og = static_cast<T*>(const_cast<void*>(p.o.ptr)) + sv.off(p.o, b) + h * p.o.sh;
 
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;  // u = c * |q.k|
@@ -402,7 +403,7 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const int N, con
         *reinterpret_cast<t4*>(og + qrow * p.o.ss + d0) = o4;
       }
     }
-    if (hh == 0) p.m[static_cast<int64_t>(bh) * N + qrow] = m_run + log2f(l_safe);
+    if (hh == 0) p.m[sv.mrow(b, h, p.Hq, p.T, p.N) + qrow] = m_run + log2f(l_safe);
   }
 }
 
@@ -412,16 +413,20 @@ template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(512) void ssa_fwd_kernel(FwdParams p) {
   constexpr int BM = 256;
   __shared__ __attribute__((aligned(1024))) char smem[4 * 2 * 64 * D * 2];
-  const int N = p.N;
-  const int nqb = (N + BM - 1) / BM;
+  const int nqb = (p.N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = L / nqb;
+  // Logical order (head, sequence, query block): each XCD's contiguous range
+  // holds a slice of heads of every sequence (balanced when packed sequences
+  // differ in length) and all blocks of one (sequence, head) share its L2.
+  const int hb = L / nqb;
   const int qb = nqb - 1 - (L % nqb);  // heaviest (last) query block first
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h / (p.Hq / p.Hkv);
+  const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
+  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
+  if (qb * BM >= sv.N) return;  // packed: past the end of a shorter document
   if (*p.n_ptr >= 0.f)
-    fwd_sp_body<T, D, CAUSAL, true>(p, N, bh, qb, b, h, hk, smem);
+    fwd_sp_body<T, D, CAUSAL, true>(p, sv, qb, b, h, hk, smem);
   else
-    fwd_sp_body<T, D, CAUSAL, false>(p, N, bh, qb, b, h, hk, smem);
+    fwd_sp_body<T, D, CAUSAL, false>(p, sv, qb, b, h, hk, smem);
 }
 
 template <typename T, int D, bool CAUSAL>

@@ -139,12 +139,14 @@ def ssa_forward_backward(q, k, v, dout, scale, n, b, causal=True, out_for_delta=
     return {"out": out, "m": m, "dq": dq, "dk": dk, "dv": dv, "dn": dn, "db": db, "delta": delta}
 
 
-def ssa_varlen_forward_backward(q, k, v, dout, cu_seqlens, scale, n, b, causal=True):
+def ssa_varlen_forward_backward(q, k, v, dout, cu_seqlens, scale, n, b, causal=True, out_for_delta=None):
     """Packed-sequence SSA: q [T, Hq, D], k/v [T, Hkv, D], cu_seqlens int [ndocs+1].
 
     Each document [cu[i], cu[i+1]) attends only within itself (block-diagonal,
     causal inside each block when ``causal``).  Returns a dict like
     ``ssa_forward_backward`` with token-major tensors ([T, H, D], m/delta [T, H]).
+    ``out_for_delta`` ([T, Hq, D]) has the meaning it has in
+    ``ssa_forward_backward``, per document.
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -171,7 +173,8 @@ def ssa_varlen_forward_backward(q, k, v, dout, cu_seqlens, scale, n, b, causal=T
         def dense(x):
             return x[a:e].transpose(1, 0, 2)[None]
 
-        r = ssa_forward_backward(dense(q), dense(k), dense(v), dense(do), scale, n, b, causal)
+        ofd = None if out_for_delta is None else dense(np.asarray(out_for_delta, dtype=np.float64))
+        r = ssa_forward_backward(dense(q), dense(k), dense(v), dense(do), scale, n, b, causal, ofd)
         res["out"][a:e] = r["out"][0].transpose(1, 0, 2)
         res["m"][a:e] = r["m"][0].T
         res["delta"][a:e] = r["delta"][0].T

@@ -130,3 +130,29 @@ def test_status_maps_to_python_exceptions():
     with pytest.raises(RuntimeError, match="launch"):
         _lib.check(_lib.SSA_ERR_LAUNCH, "ssa_fwd")
     _lib.check(_lib.SSA_OK, "ssa_fwd")
+
+
+def _varlen_fwd_args(**over):
+    a = _lib.VarlenFwdArgs(_fwd_args(), ctypes.c_void_p(FAKE), 1000)
+    a.dense.seqlen = 256
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize(
+    "field,value,status",
+    [
+        ("cu_seqlens", None, _lib.SSA_ERR_NULL_POINTER),
+        ("total_tokens", 0, _lib.SSA_ERR_CU_SEQLENS),
+        ("total_tokens", 100, _lib.SSA_ERR_CU_SEQLENS),  # max_seqlen (256) > total_tokens
+    ],
+)
+def test_varlen_fwd_validation(field, value, status):
+    a = _varlen_fwd_args(**{field: value})
+    assert _lib.lib().ssa_varlen_fwd(ctypes.byref(a), None) == status
+
+
+def test_varlen_null_args():
+    assert _lib.lib().ssa_varlen_fwd(None, None) == _lib.SSA_ERR_NULL_POINTER
+    assert _lib.lib().ssa_varlen_bwd(None, None) == _lib.SSA_ERR_NULL_POINTER
