@@ -3,9 +3,11 @@ kernels behind the reference's Python operator interface.
 
 Modules mirror the reference package ``training/train/train_ssa_triton/SSA``:
 ``ssa_flash_attention`` (autograd boundary), ``ssa_triton_kernel`` (launch
-layer names, re-exported from ``ssa_hip_kernel``).
+layer names, re-exported from ``ssa_hip_kernel``), ``ssa_attention`` (the
+attention module of ``ssa_triton_attention``, without Megatron).
 """
 
+from .ssa_attention import SSAAttention  # noqa: F401
 from .ssa_flash_attention import (  # noqa: F401
     SSAFlashAttnFunc,
     SSAFlashAttnVarlenFunc,

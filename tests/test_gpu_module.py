@@ -1,0 +1,91 @@
+"""SSAAttention (the Megatron-free module) on MI355X.
+
+Mirrors SSATritonAttention.forward (training/train/train_ssa_triton/SSA/
+ssa_triton_attention.py:132-202): [S, B, H, D] in, [S, B, Hq * D] out, grads for
+q, k, v and the learnable n (and b).  Checked against the fp64 oracle; the
+boundary is checked to be copy-free (inputs read through permuted views,
+output written in [S, B, H, D] memory order).
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ssa_oracle as so
+from parity_util import assert_parity, compare
+
+pytestmark = pytest.mark.gpu
+
+
+def _np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("learnable_b", [False, True])
+def test_module_sbhd_matches_oracle(gpu, learnable_b):
+    from SSA.ssa_attention import SSAAttention
+
+    S, B, Hq, Hkv, D = 200, 2, 8, 2, 128
+    print(f"[gpu case] module S={S} B={B} Hq={Hq} Hkv={Hkv} learnable_b={learnable_b}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(7)
+    mk = lambda h: (torch.randn(S, B, h, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu).requires_grad_()
+    q, k, v = mk(Hq), mk(Hkv), mk(Hkv)
+    mod = SSAAttention(Hq, Hkv, D, learnable_b=learnable_b).to(gpu)
+    ctx = mod(q, k, v)
+    assert ctx.shape == (S, B, Hq * D) and ctx.is_contiguous()
+    dctx = torch.randn(S, B, Hq * D, generator=g).to(torch.bfloat16).to(gpu)
+    ctx.backward(dctx)
+    torch.cuda.synchronize()
+    perm = lambda t: _np64(t).transpose(1, 2, 0, 3)  # [S,B,H,D] -> [B,H,S,D]
+    do = _np64(dctx.view(S, B, Hq, D)).transpose(1, 2, 0, 3)
+    ref = so.ssa_forward_backward(perm(q), perm(k), perm(v), do, 1.0 / math.sqrt(D), 1.5, 0.8, True)
+    got_out = ctx.view(S, B, Hq, D).permute(1, 2, 0, 3)
+    res = compare({"out": got_out, "dq": q.grad.permute(1, 2, 0, 3), "dk": k.grad.permute(1, 2, 0, 3),
+                   "dv": v.grad.permute(1, 2, 0, 3)}, ref, scalars=())
+    assert_parity(res, "module")
+    # n (and b) gradients against the kernel-level oracle of the module's own output
+    ref_k = so.ssa_forward_backward(perm(q), perm(k), perm(v), do, 1.0 / math.sqrt(D), 1.5, 0.8, True,
+                                    out_for_delta=_np64(got_out))
+    assert abs(mod.ssa_n_raw.grad.item() - ref_k["dn"]) <= 2e-3 + 2e-2 * abs(ref_k["dn"])
+    if learnable_b:
+        assert abs(mod.ssa_b_raw.grad.item() - ref_k["db"]) <= 2e-3 + 2e-2 * abs(ref_k["db"])
+
+
+def test_module_boundary_is_copy_free(gpu):
+    from SSA import ssa_hip_kernel as hk
+
+    S, B, H, D = 64, 2, 4, 64
+    x = torch.randn(S, B, H, D, device=gpu).to(torch.bfloat16)
+    view = x.permute(1, 2, 0, 3)
+    assert hk._kernel_layout(view) is view  # read in place
+    out, _ = hk.ssa_flash_attn_forward(view, view, view, 0.125, torch.tensor(1.5, device=gpu),
+                                       torch.tensor(0.8, device=gpu), True)
+    assert out.stride() == view.stride()  # written in [S, B, H, D] order
+    assert out.permute(2, 0, 1, 3).is_contiguous()
+
+
+def test_module_packed_sequences(gpu):
+    from SSA.ssa_attention import SSAAttention
+
+    lens = [37, 120, 3]
+    T, Hq, Hkv, D = sum(lens), 4, 2, 64
+    g = torch.Generator().manual_seed(11)
+    mk = lambda h: (torch.randn(T, 1, h, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu).requires_grad_()
+    q, k, v = mk(Hq), mk(Hkv), mk(Hkv)
+    cu = torch.tensor([0, 37, 157, 160], dtype=torch.int32, device=gpu)
+    psp = SimpleNamespace(cu_seqlens_q=cu, max_seqlen_q=120)
+    mod = SSAAttention(Hq, Hkv, D).to(gpu)
+    ctx = mod(q, k, v, packed_seq_params=psp)
+    assert ctx.shape == (T, 1, Hq * D)
+    ctx.float().sum().backward()
+    torch.cuda.synchronize()
+    ref = so.ssa_varlen_forward_backward(_np64(q[:, 0]), _np64(k[:, 0]), _np64(v[:, 0]),
+                                         np.ones((T, Hq, D)), cu.cpu().numpy(), 1.0 / math.sqrt(D), 1.5, 0.8, True)
+    res = compare({"out": ctx.view(T, Hq, D), "dv": v.grad[:, 0]}, ref, names=("out", "dv"), scalars=())
+    assert_parity(res, "module packed")
