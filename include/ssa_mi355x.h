@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 1
+#define SSA_ABI_VERSION 2
 
 /* Status codes. */
 enum {
@@ -92,6 +92,11 @@ typedef struct ssa_bwd_args {
   int32_t dtype;
   int32_t causal;
   float softmax_scale;
+  void* ds_workspace;   /* optional (NULL: dq recomputes the scores), 16-byte
+                           aligned, ssa_bwd_ds_workspace_bytes() bytes; when
+                           set, dkdv stores dS' there and dq reads it back, so
+                           both steps must get the same pointer.  Ignored for
+                           packed sequences (ssa_varlen_bwd recomputes). */
 } ssa_bwd_args;
 
 /* Library ABI version (SSA_ABI_VERSION). */
@@ -102,6 +107,17 @@ const char* ssa_status_string(int32_t status);
 
 /* Number of fp32 elements the `partials` workspace of ssa_bwd needs. */
 int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen);
+
+/*
+ * Bytes of the optional dS' workspace of ssa_bwd: dS' = dP (.) P / (1 + b|s|)
+ * in the input dtype, per (batch, q-head) the 32-query x 16-key tiles of the
+ * causal triangle (all tiles without the mask), 2 * N^2 bytes + O(N) per head
+ * causal, 4 * N^2 without.  With it, dk/dv writes dS' and dq becomes one
+ * streaming product dS' K instead of a recompute of the scores (the
+ * reference recomputes: ssa_triton_kernel.py:408-481, 638-719).  No
+ * reference counterpart.
+ */
+int64_t ssa_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen, int32_t causal);
 
 /*
  * Forward: out = softmax_rows(t(scale q k^T) [masked]) v, plus the base-2 row

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "ssa_abi_version",
     "ssa_status_string",
     "ssa_bwd_partials_count",
+    "ssa_bwd_ds_workspace_bytes",
     "ssa_fwd",
     "ssa_bwd",
     "ssa_bwd_preprocess",
@@ -41,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "ssa_varlen_bwd",
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Tensor4(ctypes.Structure):
@@ -98,6 +99,7 @@ class BwdArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("causal", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
+        ("ds_workspace", ctypes.c_void_p),
     ]
 
 
@@ -120,6 +122,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssa_status_string.argtypes = [ctypes.c_int32]
     lib.ssa_bwd_partials_count.restype = ctypes.c_int64
     lib.ssa_bwd_partials_count.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    lib.ssa_bwd_ds_workspace_bytes.restype = ctypes.c_int64
+    lib.ssa_bwd_ds_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
     for name, argt in (("ssa_fwd", FwdArgs), ("ssa_bwd", BwdArgs), ("ssa_bwd_preprocess", BwdArgs),
                        ("ssa_bwd_dkdv", BwdArgs), ("ssa_bwd_dq", BwdArgs), ("ssa_bwd_reduce", BwdArgs)):
         fn = getattr(lib, name)

@@ -21,7 +21,11 @@ device (no host synchronisation); ``dn`` / ``db`` come back as 0-d fp32 tensors.
 
 Differences from the reference, all widening: any sequence length (the
 reference's backward needs N % 128 == 0), and results are bitwise
-reproducible.  Errors: ``AssertionError`` for ``Hq % Hkv != 0`` and a
+reproducible.  By default the backward keeps dS' (the score gradient, input
+dtype, causal triangle only: 2 N^2 bytes per (batch, head)) in a transient
+workspace so that dQ is one streaming product with K instead of the
+reference's recompute of the scores; ``SSA_BWD_DS=0`` (or a workspace above
+``SSA_BWD_DS_MAX_BYTES``, default 16 GiB) selects the recompute.  Errors: ``AssertionError`` for ``Hq % Hkv != 0`` and a
 non-power-of-two head dim, as in the reference; ``ValueError`` for head dims
 other than 32/64/128 and dtypes other than bf16/fp16.
 """
@@ -29,6 +33,7 @@ other than 32/64/128 and dtypes other than bf16/fp16.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -107,17 +112,30 @@ def ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True):
     return out, m
 
 
+def _use_ds_workspace(nbytes: int, ds) -> bool:
+    """Whether the backward keeps dS' in a workspace of ``nbytes`` bytes
+    (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy)."""
+    if ds is not None:
+        return bool(ds)
+    mode = os.environ.get("SSA_BWD_DS", "auto").strip().lower()
+    if mode in ("0", "off", "false", "no"):
+        return False
+    limit = int(os.environ.get("SSA_BWD_DS_MAX_BYTES", str(16 << 30)))
+    return mode in ("1", "on", "true", "yes") or nbytes <= limit
+
+
 class BackwardLaunch:
     """Validated backward arguments plus every buffer they point to.
 
     ``run()`` enqueues the whole backward (``ssa_bwd``); ``run_stage(name)``
     enqueues one of ``preprocess``, ``dkdv``, ``dq``, ``reduce`` (in that order)
-    so callers can time or schedule the kernels separately.
+    so callers can time or schedule the kernels separately.  ``ds`` selects the
+    dS' workspace (True / False; None: the ``SSA_BWD_DS`` policy).
     """
 
     STAGES = ("preprocess", "dkdv", "dq", "reduce")
 
-    def __init__(self, q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True):
+    def __init__(self, q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True, ds=None):
         B, Hq, Hkv, N, D = _check_inputs(q, k, v)
         if tuple(out.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape):
             raise ValueError("out and dout must have the shape of q")
@@ -141,6 +159,9 @@ class BackwardLaunch:
         self.partials = torch.empty(count, device=dev, dtype=torch.float32)
         self.dn = torch.empty((), device=dev, dtype=torch.float32)
         self.db = torch.empty((), device=dev, dtype=torch.float32)
+        ds_bytes = int(self.lib.ssa_bwd_ds_workspace_bytes(B, Hq, N, int(bool(causal))))
+        self.ds = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
+                   if _use_ds_workspace(ds_bytes, ds) else None)
         self.device = dev
         self.args = _lib.BwdArgs(
             _t4(self.q), _t4(self.k), _t4(self.v), _t4(self.out), _t4(self.dout),
@@ -148,6 +169,7 @@ class BackwardLaunch:
             self.m.data_ptr(), self.delta.data_ptr(), self.partials.data_ptr(),
             self.dn.data_ptr(), self.db.data_ptr(), self.n32.data_ptr(), self.b32.data_ptr(),
             B, Hq, Hkv, N, D, _DTYPES[q.dtype], int(bool(causal)), float(softmax_scale),
+            self.ds.data_ptr() if self.ds is not None else None,
         )
 
     def _call(self, fn_name: str) -> None:
@@ -169,9 +191,10 @@ class BackwardLaunch:
         return self.dq, self.dk, self.dv, self.dn, self.db
 
 
-def ssa_flash_attn_backward(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True):
-    """SSA attention backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors."""
-    launch = BackwardLaunch(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal)
+def ssa_flash_attn_backward(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True, ds=None):
+    """SSA attention backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors.
+    ``ds``: keep dS' in a workspace (True / False; None: the ``SSA_BWD_DS`` policy)."""
+    launch = BackwardLaunch(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal, ds)
     launch.run()
     return launch.results()
 

@@ -82,6 +82,8 @@ int32_t fill_bwd(const ssa_bwd_args* a, ssa::BwdParams* p, bool preprocess_only)
   p->scale = a->softmax_scale;
   p->cu_seqlens = nullptr;
   p->T = 0;
+  if (!preprocess_only && a->ds_workspace != nullptr && !aligned16(a->ds_workspace)) return SSA_ERR_ALIGNMENT;
+  p->ds = preprocess_only ? nullptr : a->ds_workspace;
   return SSA_OK;
 }
 
@@ -149,6 +151,11 @@ int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen) 
   return 2ll * batch * heads_kv * ssa::dkdv_key_blocks(seqlen);
 }
 
+int64_t ssa_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen, int32_t causal) {
+  if (batch <= 0 || heads_q <= 0 || seqlen <= 0) return 0;
+  return static_cast<int64_t>(batch) * heads_q * ssa::ds_tiles_per_head(seqlen, causal != 0) * 1024;
+}
+
 int32_t ssa_fwd(const ssa_fwd_args* a, void* stream) {
   ssa::FwdParams p{};
   SSA_TRY(fill_fwd(a, &p));
@@ -176,6 +183,7 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
   p.cu_seqlens = va->cu_seqlens;
   p.T = va->total_tokens;
+  p.ds = nullptr;  // packed batches recompute dQ
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool causal = a->causal != 0;
   // Delta over the whole token stream: one sequence of T rows, [H, T] layout.

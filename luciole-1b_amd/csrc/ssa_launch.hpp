@@ -17,4 +17,18 @@ hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 // Number of key blocks of the dK/dV kernel (each writes one dn and one db partial).
 __host__ __device__ inline int dkdv_key_blocks(int N) { return (N + 127) / 128; }
 
+// dS' workspace: per (b, q-head) a sequence of 1 KB tiles, each 32 queries x
+// 16 keys of dS' in bf16/fp16, 16 bytes per lane of the writing wave (lane
+// 16 g + kl: key kl, queries 16 t + 4 g + (0..3) in elements 4 t ..).  Query
+// tile qi (rows 32 qi ..) holds key tiles kj = 0 .. 2 qi + 1 under the causal
+// mask (the triangle), kj = 0 .. 2 nq32 - 1 without it.
+__host__ __device__ inline int64_t ds_tiles_per_head(int N, bool causal) {
+  const int64_t nq = (N + 31) / 32;
+  return causal ? nq * (nq + 1) : 2 * nq * nq;
+}
+__host__ __device__ inline int64_t ds_row_offset(int qi, int N, bool causal) {
+  const int64_t q = qi;
+  return causal ? q * (q + 1) : q * 2 * ((N + 31) / 32);
+}
+
 }  // namespace ssa

@@ -53,6 +53,38 @@ def test_partials_count():
     assert lib.ssa_bwd_partials_count(0, 1, 1) == 0
 
 
+def _ds_tiles_needed(N, causal):
+    """1 KB dS' tiles (32 queries x 16 keys) holding at least one unmasked pair."""
+    need = 0
+    for qi in range((N + 31) // 32):
+        for kj in range((N + 15) // 16):
+            qmax = min(32 * qi + 31, N - 1)
+            if 16 * kj < N and (not causal or 16 * kj <= qmax):
+                need += 1
+    return need
+
+
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 100, 256, 511])
+@pytest.mark.parametrize("causal", [0, 1])
+def test_ds_workspace_bytes(N, causal):
+    lib = _lib.lib()
+    nq = (N + 31) // 32
+    per_head = nq * (nq + 1) if causal else 2 * nq * nq
+    assert lib.ssa_bwd_ds_workspace_bytes(3, 5, N, causal) == 3 * 5 * per_head * 1024
+    # every tile the mask needs fits in its query row, and causal rows hold
+    # nothing else when N is a multiple of 32
+    assert _ds_tiles_needed(N, causal) <= per_head
+    if causal and N % 32 == 0:
+        assert _ds_tiles_needed(N, causal) == per_head
+
+
+def test_ds_workspace_bytes_headline_and_empty():
+    lib = _lib.lib()
+    assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 4096, 1) == 4 * 16 * 128 * 129 * 1024
+    assert lib.ssa_bwd_ds_workspace_bytes(0, 16, 4096, 1) == 0
+    assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 0, 0) == 0
+
+
 FAKE = 0x10000  # 16-byte aligned, never dereferenced
 
 
@@ -110,6 +142,7 @@ def test_fwd_null_args():
         ("partials", None, _lib.SSA_ERR_NULL_POINTER),
         ("dn", None, _lib.SSA_ERR_NULL_POINTER),
         ("dq", _lib.Tensor4(FAKE, 4, 0, 128), _lib.SSA_ERR_ALIGNMENT),
+        ("ds_workspace", FAKE + 8, _lib.SSA_ERR_ALIGNMENT),
     ],
 )
 def test_bwd_validation(entry, field, value, status):

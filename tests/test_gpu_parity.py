@@ -20,7 +20,8 @@ from parity_util import assert_parity, compare, make_inputs, oracle_fwd_bwd, sca
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, B, Hq, Hkv, N, D, dtype, causal, layout="contig", n_val=1.5, b_val=0.8, seed=1234, qkv_scale=1.0):
+def _run(gpu, B, Hq, Hkv, N, D, dtype, causal, layout="contig", n_val=1.5, b_val=0.8, seed=1234, qkv_scale=1.0,
+         ds=None):
     """Forward + backward through the reference-named API, checked two ways.
 
     res_exact -- out, dq, dk, dv against the exact fp64 function of (q, k, v, dO)
@@ -32,14 +33,14 @@ def _run(gpu, B, Hq, Hkv, N, D, dtype, causal, layout="contig", n_val=1.5, b_val
     from SSA.ssa_triton_kernel import ssa_flash_attn_backward, ssa_flash_attn_forward
 
     label = (f"B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} {str(dtype)[6:]} causal={int(causal)} "
-             f"{layout} n={n_val} b={b_val}")
+             f"{layout} n={n_val} b={b_val} dq={'default' if ds is None else ('ds' if ds else 'recompute')}")
     print(f"[gpu case] {label}", file=sys.stderr, flush=True)
     q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, gpu, layout, seed, qkv_scale)
     scale = scale_for(D)
     n = torch.tensor(n_val, dtype=torch.float32, device=gpu)
     b = torch.tensor(b_val, dtype=torch.float32, device=gpu)
     out, m = ssa_flash_attn_forward(q, k, v, scale, n, b, causal=causal)
-    dq, dk, dv, dn, db = ssa_flash_attn_backward(q, k, v, out, do, m, scale, n, b, causal=causal)
+    dq, dk, dv, dn, db = ssa_flash_attn_backward(q, k, v, out, do, m, scale, n, b, causal=causal, ds=ds)
     torch.cuda.synchronize()
     got = {"out": out, "dq": dq, "dk": dk, "dv": dv, "dn": dn.item(), "db": db.item()}
     ref = oracle_fwd_bwd(q, k, v, do, scale, n_val, b_val, causal)
@@ -65,14 +66,17 @@ def _check(label, res_exact, res_kernel, mres):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("heads", [(4, 4), (8, 2)])
-def test_parity_matrix(gpu, D, dtype, causal, heads):
-    _check(*_run(gpu, 1, heads[0], heads[1], 256, D, dtype, causal))
+@pytest.mark.parametrize("dq_path", ["ds", "recompute"])
+def test_parity_matrix(gpu, D, dtype, causal, heads, dq_path):
+    _check(*_run(gpu, 1, heads[0], heads[1], 256, D, dtype, causal, ds=dq_path == "ds"))
 
 
 @pytest.mark.parametrize("N", [1, 7, 64, 129, 200, 511])
 @pytest.mark.parametrize("D", [64, 128])
-def test_parity_ragged_lengths(gpu, N, D):
-    _check(*_run(gpu, 2, 4, 2, N, D, torch.bfloat16, True))
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dq_path", ["ds", "recompute"])
+def test_parity_ragged_lengths(gpu, N, D, causal, dq_path):
+    _check(*_run(gpu, 2, 4, 2, N, D, torch.bfloat16, causal, ds=dq_path == "ds"))
 
 
 @pytest.mark.parametrize("layout", ["contig", "strided"])
