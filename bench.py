@@ -9,6 +9,9 @@ n=1.5, b=0.8, scale=1/sqrt(D) (the shape BASELINE.json's metric is quoted on).
 
 value = algorithmic fwd+bwd FLOPs / step time, with fwd = 4 D pairs and
 bwd = 10 D pairs (pairs = unmasked (q, k) pairs), i.e. 14 D pairs per step.
+The backward runs the library's default path: dS' kept in a workspace
+(ssa_bwd_ds_workspace_bytes) and dQ as a streaming dS' K product; set
+SSA_BWD_DS=0 to time the recompute path instead (config.bwd_path says which).
 
 Also reported on the same JSON line:
   roofline     -- the dominant kernel's algorithmic FLOPs (or bytes) per launch
@@ -245,24 +248,31 @@ def main():
         kernels[f"ssa_bwd_{stage}_kernel"] = {"avg_ms": avg, "median_ms": med}
     # Algorithmic work per launch: dK/dV does QK^T, dP, dV, dK (8 D per pair);
     # dQ adds only its dQ product (2 D per pair); preprocess moves O, dO, Delta.
+    # On the dS' workspace path dQ streams the workspace (read once) plus K and
+    # writes dQ: bytes are its bound, its FLOPs are reported alongside.
+    ds_bytes = launch.ds.numel() if launch.ds is not None else 0
     kernels["ssa_bwd_dkdv_kernel"]["alg_flop"] = 8 * D * pairs
     kernels["ssa_bwd_dq_kernel"]["alg_flop"] = 2 * D * pairs
     esize = 2
+    if ds_bytes:
+        kernels["ssa_bwd_dq_kernel"]["alg_bytes"] = ds_bytes + (B * Hkv + B * Hq) * S * D * esize
     pre_bytes = 2 * B * Hq * S * D * esize + 4 * B * Hq * S
     kernels["ssa_bwd_preprocess_kernel"]["alg_bytes"] = pre_bytes
     for name, kd in kernels.items():
         if "alg_flop" in kd:
             kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
             kd["frac_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
+            kd["bound"] = "mfma"
         if "alg_bytes" in kd:
             kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
             kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
+            kd["bound"] = "hbm"
     traffic = measured_traffic(args.config) if args.dtype == "bf16" else {}
     for name, kd in kernels.items():
         kd["hbm_bytes"] = traffic.get(name)
     dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
     kd = kernels[dominant]
-    if "tflops" in kd:
+    if kd.get("bound") == "mfma":
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": kd["tflops"] / PEAK_BF16_TFLOPS, "traffic": kd["hbm_bytes"],
                     "avg_launch_ms": kd["avg_ms"]}
@@ -288,7 +298,8 @@ def main():
         "data": "synthetic: Q/K/V = 0.5 N(0,1), dO ~ N(0,1), seed 1234, n=1.5, b=0.8",
         "config": {"workload": f"SSA attention fwd+bwd ({args.config})", "B": B, "Hq": Hq, "Hkv": Hkv,
                    "S": S, "D": D, "causal": causal, "pairs": pairs,
-                   "alg_gflop_per_step": (flops_fwd + flops_bwd) / 1e9},
+                   "alg_gflop_per_step": (flops_fwd + flops_bwd) / 1e9,
+                   "bwd_path": "ds_workspace" if ds_bytes else "recompute", "ds_workspace_bytes": ds_bytes},
         "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
         "fwd_tflops": flops_fwd / (fwd_ms * 1e-3) / 1e12,
         "bwd_tflops": flops_bwd / (bwd_ms * 1e-3) / 1e12,

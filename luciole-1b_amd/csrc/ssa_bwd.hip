@@ -560,12 +560,14 @@ __global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
   };
   StepPos ip{0, 0, 0};  // next step to load
   issue(ip);
-  // B operands of S^T / dP^T: key l16, columns 32 ks + 8 g4 .. + 8
+  // B operands of S^T / dP^T: key l16, columns 32 ks + 8 row16_chunk(g4) .. + 8
+  // (the column order of the Row16Base fetches of Q and dO)
   v8 kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    kf[ks] = key < N ? load16<v8>(kg + key * p.k.ss + ks * 32 + 8 * g4) : zero8<v8>();
-    vf[ks] = key < N ? load16<v8>(vg + key * p.v.ss + ks * 32 + 8 * g4) : zero8<v8>();
+    const int col = ks * 32 + 8 * row16_chunk(g4);
+    kf[ks] = key < N ? load16<v8>(kg + key * p.k.ss + col) : zero8<v8>();
+    vf[ks] = key < N ? load16<v8>(vg + key * p.v.ss + col) : zero8<v8>();
   }
   wait_vm<0>();  // sub-tile 0 and the K/V fragments
   for (int st = 1; st < PF; ++st) {
@@ -710,7 +712,7 @@ __global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
   };
 
   // steady state: 32 fenced ticks, MFMA g at tick g * 32 / NG with its operand
-  // reads two MFMAs ahead; element e of S_j runs A at tick 4e - 8, B at 4e - 3,
+  // reads RA MFMAs ahead; element e of S_j runs A at tick 4e - 8, B at 4e - 3,
   // C1 at 4e + 2, C2 at 4e + 3.
   auto slot_fast = [&](int j) {
     constexpr int NG = 2 * DT + 4 * KS;  // dV, dK per column tile; S, dP per row tile and k-step
@@ -727,19 +729,22 @@ __global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
       mq[t] = lds_read_f4(ml + (16 * t + 4 * g4) * 4);
       dq4[t] = lds_read_f4(ml + 128 + (16 * t + 4 * g4) * 4);
     }
-    v8 ops[3];
+    // operand reads run RA MFMAs ahead, through a ring of RA + 1 registers
+    constexpr int RA = 4, NO = RA + 1;
+    v8 ops[NO];
     // MFMA g < 2 DT: dV (even) / dK (odd) for tile dt = g / 2; else S (even) /
-    // dP (odd) over k-step and row tile: h = g - 2 DT, pair = h / 2 -> (t, ks).
+    // dP (odd), h = g - 2 DT: k-step ks = h / 4, row tile t = h / 2 % 2 (each
+    // accumulator's chain of k-steps 4 MFMAs apart).
     auto read = [&](auto gc) {
       constexpr int Gi = decltype(gc)::value;
       if constexpr (Gi < 2 * DT) {
         constexpr int dt = Gi / 2;
         const Tr16Base& tr = (Gi % 2 == 0) ? td : tq;
-        ops[Gi % 3] = __builtin_shufflevector(tile_read_tr16<v4>(tr, dt, 0), tile_read_tr16<v4>(tr, dt, 1), 0, 1, 2,
-                                              3, 4, 5, 6, 7);
+        ops[Gi % NO] = __builtin_shufflevector(tile_read_tr16<v4>(tr, dt, 0), tile_read_tr16<v4>(tr, dt, 1), 0, 1, 2,
+                                               3, 4, 5, 6, 7);
       } else if constexpr (Gi < NG) {
-        constexpr int h = Gi - 2 * DT, pr = h / 2, t = pr / KS, ks = pr % KS;
-        ops[Gi % 3] = tile_read_row16<v8>((h % 2 == 0) ? rq : rd, ks, t);
+        constexpr int h = Gi - 2 * DT, ks = h / 4, t = (h / 2) % 2;
+        ops[Gi % NO] = tile_read_row16<v8>((h % 2 == 0) ? rq : rd, ks, t);
       }
     };
     auto mfma = [&](auto gc) {
@@ -747,15 +752,15 @@ __global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
       if constexpr (Gi < 2 * DT) {
         constexpr int dt = Gi / 2;
         if constexpr (Gi % 2 == 0)
-          dv[dt] = mfma16(pa, ops[Gi % 3], dv[dt]);
+          dv[dt] = mfma16(pa, ops[Gi % NO], dv[dt]);
         else
-          dk[dt] = mfma16(sa, ops[Gi % 3], dk[dt]);
+          dk[dt] = mfma16(sa, ops[Gi % NO], dk[dt]);
       } else {
-        constexpr int h = Gi - 2 * DT, pr = h / 2, t = pr / KS, ks = pr % KS;
+        constexpr int h = Gi - 2 * DT, ks = h / 4, t = (h / 2) % 2;
         if constexpr (h % 2 == 0)
-          sn[t] = mfma16(ops[Gi % 3], kf[ks], ks == 0 ? f32x4{} : sn[t]);
+          sn[t] = mfma16(ops[Gi % NO], kf[ks], ks == 0 ? f32x4{} : sn[t]);
         else
-          dn2[t] = mfma16(ops[Gi % 3], vf[ks], ks == 0 ? f32x4{} : dn2[t]);
+          dn2[t] = mfma16(ops[Gi % NO], vf[ks], ks == 0 ? f32x4{} : dn2[t]);
       }
     };
     float Lv[8], rv[8], slv[8], pv[8], ddv[8], dtv[8], dsv[8];
@@ -797,7 +802,7 @@ __global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
     auto tick = [&](auto tc) {
       constexpr int t = decltype(tc)::value;
       if constexpr (t % STRIDE == 0) {
-        read(std::integral_constant<int, t / STRIDE + 2>{});
+        read(std::integral_constant<int, t / STRIDE + RA>{});
         mfma(std::integral_constant<int, t / STRIDE>{});
       }
       constexpr int e = t / 4, ph = t % 4;
@@ -812,8 +817,9 @@ __global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);
     };
-    read(std::integral_constant<int, 0>{});
-    read(std::integral_constant<int, 1>{});
+    [&]<int... r>(std::integer_sequence<int, r...>) {
+      (read(std::integral_constant<int, r>{}), ...);
+    }(std::make_integer_sequence<int, RA>{});
     A(0);
     A(1);
     B(0);

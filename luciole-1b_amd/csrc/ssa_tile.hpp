@@ -42,13 +42,15 @@ struct BlockLayout {
 // 2^24 elements (checked on the host) keep every offset under 2^31.
 //
 // Two row swizzles: 4 (c & 3) for the 32x32 operand fetches (RowBase,
-// TrBase), and 8 (c & 1) + 4 (c >> 1 & 1) for the 16x16 ones (Row16Base,
-// Tr16Base), whose transpose reads take rows 4 g .. 4 g + 3 of chunks 2 dt and
-// 2 dt + 1 in one half-wave: the second swizzle sends the two chunks' rows
-// 0..7 to disjoint positions, so each half-wave covers all banks once.
+// TrBase), and 8 (c & 1) for the 16x16 ones (Row16Base, Tr16Base).  Measured
+// on gfx950: the LDS serves each half-wave (32 lanes) of a read together; a
+// 16-byte read is at full rate when the two 16-lane groups of a half-wave
+// apply the same permutation to their 256-byte windows, and an 8-byte
+// transpose read when the two chunks a 16-lane group touches (columns
+// 16 dt .. 16 dt + 15) land on different banks, which 8 (c & 1) gives.
 enum class Swizzle { k32, k16 };
 __device__ __forceinline__ constexpr int row_swizzle(Swizzle sw, int c3) {
-  return sw == Swizzle::k32 ? 4 * c3 : 8 * (c3 & 1) + 4 * (c3 >> 1);
+  return sw == Swizzle::k32 ? 4 * c3 : 8 * (c3 & 1);
 }
 struct LoadLane {
   uint32_t off;   // r * row stride + half * 16, bytes
@@ -208,18 +210,21 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
 // ---- operand fetches for 16x16x32 MFMAs from a 32-row block (BlockLayout) ----
 //
 // Tiles read with these are loaded with Swizzle::k16: row r of chunk c sits at
-// position r ^ s(c), s(c) = 8 (c & 1) + 4 (c >> 1 & 1).
+// position r ^ 8 (c & 1).
 //
 // Row-wise operand (A of an M=16 product, k over the columns): lane
-// (g = lane / 16, i = lane % 16) fetches row 16 t + i, chunk 4 ks + g, at
-// position 16 t + (i ^ s(g)): one per-lane base plus the immediate
-// ks * 2048 + t * 256 (+ block offset).  Each group of 16 lanes reads 256
-// contiguous bytes: no bank conflicts.
+// (g = lane / 16, i = lane % 16) fetches row 16 t + i of chunk 4 ks + row16_chunk(g),
+// i.e. k-slots 8 g .. 8 g + 7 hold columns 32 ks + 8 row16_chunk(g) ..; the
+// other operand of the product must use the same column order.  The
+// permutation (0, 2, 1, 3) puts chunks of equal parity in each half-wave, so
+// both 16-lane groups of a half-wave apply the same row permutation (full
+// rate).  Address: one per-lane base plus the immediate ks * 2048 + t * 256.
+__device__ __forceinline__ constexpr int row16_chunk(int g) { return 2 * (g & 1) + (g >> 1); }
 struct Row16Base {
   uint32_t b;
   __device__ __forceinline__ explicit Row16Base(int lane) {
-    const int g = lane >> 4, i = lane & 15;
-    b = static_cast<uint32_t>(g * 512 + ((i ^ row_swizzle(Swizzle::k16, g)) << 4));
+    const int c = row16_chunk(lane >> 4), i = lane & 15;
+    b = static_cast<uint32_t>(c * 512 + ((i ^ row_swizzle(Swizzle::k16, c)) << 4));
   }
 };
 __device__ __forceinline__ Row16Base at_tile(const Row16Base& rb, uint32_t lds) {
@@ -238,33 +243,27 @@ __device__ __forceinline__ V tile_read_row16(const Row16Base& rb, int ks, int t)
 //   q(8 g + 4 t + i) = 16 t + 4 g + i,
 // the row order in which a 16x16 accumulator holds a [32 x 16] block's two
 // row tiles.  Lane i of a group supplies row 16 t + 4 g + i / 4 and columns
-// 16 dt + 4 (i % 4) .. + 3 (8 bytes), chunk c = 2 dt + ch (ch = i % 4 / 2);
-// with c & 3 = 2 (dt & 1) + ch the swizzle depends on the parity of dt.
-// Half-wave g in {0, 1} (or {2, 3}) reads rows 4 g + (0..3) of both chunks at
-// positions 4 (g ^ (2 ch + dt & 1)) + (0..3): four disjoint row groups, 256
-// bytes, every bank once.
+// 16 dt + 4 (i % 4) .. + 3 (8 bytes), chunk c = 2 dt + ch (ch = i % 4 / 2),
+// at position (4 g + i / 4) ^ 8 ch: the two chunks of a group on different
+// banks.
 struct Tr16Base {
-  uint32_t b[2];
+  uint32_t b;
   __device__ __forceinline__ explicit Tr16Base(int lane) {
     const int g = lane >> 4, i = lane & 15, ch = (i & 3) >> 1;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int pos = (4 * g + (i >> 2)) ^ row_swizzle(Swizzle::k16, 2 * p + ch);
-      b[p] = static_cast<uint32_t>(ch * 512 + (pos << 4) + ((i & 1) << 3));
-    }
+    const int pos = (4 * g + (i >> 2)) ^ row_swizzle(Swizzle::k16, ch);
+    b = static_cast<uint32_t>(ch * 512 + (pos << 4) + ((i & 1) << 3));
   }
 };
 __device__ __forceinline__ Tr16Base at_tile(const Tr16Base& tb, uint32_t lds) {
   Tr16Base r = tb;
-  r.b[0] = opaque(tb.b[0] + lds);
-  r.b[1] = opaque(tb.b[1] + lds);
+  r.b = opaque(tb.b + lds);
   return r;
 }
 template <typename V4>
 __device__ __forceinline__ V4 tile_read_tr16(const Tr16Base& tb, int dt, int t) {
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
   const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-      (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(tb.b[dt & 1] + dt * 1024 + t * 256));
+      (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(tb.b + dt * 1024 + t * 256));
   return __builtin_bit_cast(V4, v);
 }
 
