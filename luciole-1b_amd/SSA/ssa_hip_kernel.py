@@ -21,11 +21,13 @@ device (no host synchronisation); ``dn`` / ``db`` come back as 0-d fp32 tensors.
 
 Differences from the reference, all widening: any sequence length (the
 reference's backward needs N % 128 == 0), and results are bitwise
-reproducible.  By default the backward keeps dS' (the score gradient, input
-dtype, causal triangle only: 2 N^2 bytes per (batch, head)) in a transient
-workspace so that dQ is one streaming product with K instead of the
-reference's recompute of the scores; ``SSA_BWD_DS=0`` (or a workspace above
-``SSA_BWD_DS_MAX_BYTES``, default 16 GiB) selects the recompute.  Errors: ``AssertionError`` for ``Hq % Hkv != 0`` and a
+reproducible.  For head dim 128 the backward by default keeps dS' (the score
+gradient, input dtype, causal triangle only: 2 N^2 bytes per (batch, head)) in
+a transient workspace so that dQ is one streaming product with K instead of
+the reference's recompute of the scores (measured faster at D = 128, slower at
+D = 64, where the recompute is cheap); ``SSA_BWD_DS=0`` / ``1`` forces either
+path, and a workspace above ``SSA_BWD_DS_MAX_BYTES`` (default 16 GiB) always
+recomputes.  Errors: ``AssertionError`` for ``Hq % Hkv != 0`` and a
 non-power-of-two head dim, as in the reference; ``ValueError`` for head dims
 other than 32/64/128 and dtypes other than bf16/fp16.
 """
@@ -112,16 +114,19 @@ def ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True):
     return out, m
 
 
-def _use_ds_workspace(nbytes: int, ds) -> bool:
+def _use_ds_workspace(nbytes: int, head_dim: int, ds) -> bool:
     """Whether the backward keeps dS' in a workspace of ``nbytes`` bytes
-    (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy)."""
+    (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy: on for
+    head dim 128 within ``SSA_BWD_DS_MAX_BYTES``)."""
     if ds is not None:
         return bool(ds)
     mode = os.environ.get("SSA_BWD_DS", "auto").strip().lower()
     if mode in ("0", "off", "false", "no"):
         return False
+    if mode in ("1", "on", "true", "yes"):
+        return True
     limit = int(os.environ.get("SSA_BWD_DS_MAX_BYTES", str(16 << 30)))
-    return mode in ("1", "on", "true", "yes") or nbytes <= limit
+    return head_dim == 128 and nbytes <= limit
 
 
 class BackwardLaunch:
@@ -161,7 +166,7 @@ class BackwardLaunch:
         self.db = torch.empty((), device=dev, dtype=torch.float32)
         ds_bytes = int(self.lib.ssa_bwd_ds_workspace_bytes(B, Hq, N, int(bool(causal))))
         self.ds = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-                   if _use_ds_workspace(ds_bytes, ds) else None)
+                   if _use_ds_workspace(ds_bytes, D, ds) else None)
         self.device = dev
         self.args = _lib.BwdArgs(
             _t4(self.q), _t4(self.k), _t4(self.v), _t4(self.out), _t4(self.dout),

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_kernel(BwdParams p) {
 // issues vector work.  Sub-tiles (Q, dO, M, Delta) live in four LDS buffers:
 // sub-tile t is loaded in slot t - 2 (its buffer last held t - 4, read for
 // the last time in slot t - 3) and complete at the start of slot t - 1.
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, bool DS>
 __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
@@ -262,6 +262,27 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       sa[ks] = sa2[ks];
     }
   };
+  // dS' of sub-tile st to the workspace (DS): this wave's 32 keys are key
+  // tiles kj0 = k0w / 16 and kj0 + 1 of query tile q0 / 32 (both inside the
+  // causal triangle when the sub-tile is not skipped).  Lane (l32, hh) holds
+  // key l32 and, in sa2[ks], queries 16 ks + 4 hh + (0..3) (elements 0..3) and
+  // 16 ks + 8 + 4 hh + (0..3) (elements 4..7): in the tile format (lane
+  // 16 g + kl: key kl, queries 16 t + 4 g + (0..3) at elements 4 t ..) these
+  // are four 8-byte pieces, g = hh or 2 + hh, t = ks.
+  auto ds_store = [&](int st) {
+    int g;
+    const int q0 = step_q0(st, g);
+    const int hq = hk * G + g;
+    const int64_t tile = (static_cast<int64_t>(b) * p.Hq + hq) * ds_tiles_per_head(N, CAUSAL) +
+                         ds_row_offset(q0 >> 5, N, CAUSAL) + (k0w >> 4);
+    T* dst = static_cast<T*>(p.ds) + tile * 512 + (l32 >> 4) * 512 + (l32 & 15) * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      *reinterpret_cast<v4*>(dst + (16 * hh) * 8 + 4 * ks) = __builtin_shufflevector(sa2[ks], sa2[ks], 0, 1, 2, 3);
+      *reinterpret_cast<v4*>(dst + (16 * (2 + hh)) * 8 + 4 * ks) =
+          __builtin_shufflevector(sa2[ks], sa2[ks], 4, 5, 6, 7);
+    }
+  };
   auto slot_generic = [&](int j) {
     wait_vm<0>();  // sub-tile j + 1
     __builtin_amdgcn_s_barrier();
@@ -273,6 +294,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         elementwise(j, std::true_type{});
       else
         elementwise(j, std::false_type{});
+      if constexpr (DS) ds_store(j);
     }
     rotate();
   };
@@ -391,6 +413,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       (tick(std::integral_constant<int, t>{}), ...);
     }(std::make_integer_sequence<int, 32>{});
     kahan(tdn, tdb);
+    if constexpr (DS) ds_store(j);
     rotate();
   };
 
@@ -437,444 +460,6 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
     const float sdn = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
     const float sdb = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    p.partials[static_cast<int64_t>(bhk) * nkb + kb] = kLn2 * sdn;
-    p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = n * p.scale * sdb;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dK, dV with 16 keys per wave on 16x16x32 MFMAs: 8 waves (two per SIMD) for
-// a block of 128 keys, so the dK/dV accumulators take 64 registers per wave
-// and two waves share each SIMD.  Per 32-query sub-tile and wave:
-//   S^T, dP^T (32 queries x 16 keys, two 16x16 tiles each): A = Q / dO rows
-//     from LDS, B = K / V fragments of the wave's keys held in registers;
-//   the accumulators hold, per lane, key l%16 and queries 16t + 4g + i, which
-//     is the A operand of dV += P dO and dK += dS' Q with the contraction
-//     index in that order; the B operands (dO, Q) are LDS transpose reads that
-//     deliver the same row order (Tr16Base).
-// Same step order, buffers and software pipeline as the 32-key kernel.
-template <typename T, int D, bool CAUSAL, bool DS>
-__global__ __launch_bounds__(512) void ssa_bwd_dkdv16_kernel(BwdParams p) {
-  typedef typename Vec8<T>::type v8;
-  typedef T v4 __attribute__((ext_vector_type(4)));
-  constexpr int BN = 128, BMQ = 32, NB = 8, PF = 6, NW = 8;  // PF: sub-tiles loaded ahead
-  constexpr int KS = D / 32, DT = D / 16;  // k-steps of S/dP, 16-column tiles of dK/dV
-  constexpr int TILE = BMQ * D * 2;
-  constexpr int BUF = 2 * TILE + 256;  // Q, dO, M[32], Delta[32]
-  __shared__ __attribute__((aligned(1024))) char smem[NB * BUF];
-  __shared__ float red[2][NW];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15, g4 = lane >> 4;
-  const int nkb = dkdv_key_blocks(p.N);
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int bhk = L / nkb;
-  const int kb = L % nkb;
-  const int b = bhk % p.B, hk = bhk / p.B;
-  const int G = p.Hq / p.Hkv;
-  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
-  const int N = sv.N;
-  if (kb * BN >= N) {  // packed: past the end of a shorter document
-    if (tid == 0) {
-      const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
-      p.partials[static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
-      p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
-    }
-    return;
-  }
-  const float n = *p.n_ptr;
-  const float c = p.scale * *p.b_ptr;
-  const uint32_t lds0 = lds_addr(smem);
-  const Row16Base rb(lane);
-  const Tr16Base tb(lane);
-  const LoadLane llq(lane, wave, p.q.ss, Swizzle::k16), lld(lane, wave, p.dout.ss, Swizzle::k16);
-  // direct loads this wave issues per sub-tile: its 1 KB pieces of Q and dO,
-  // plus M/Delta on the last wave
-  constexpr int NPIECE = BlockLayout<D>::IPB;
-  const int lw = 2 * (NPIECE >= NW ? NPIECE / NW : (wave < NPIECE ? 1 : 0)) + (wave == NW - 1 ? 1 : 0);
-
-  const int k0 = kb * BN;
-  const int kw = k0 + wave * 16;
-  const int key = kw + l16;
-  const T* kg = static_cast<const T*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
-  const T* vg = static_cast<const T*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
-
-  const int qstart = CAUSAL ? k0 : 0;
-  const int nsub = (N - qstart + BMQ - 1) / BMQ;
-  const int nsteps = G * nsub;
-  const bool key_edge = k0 + BN > N;
-  const int nlo = key_edge ? nsub : (CAUSAL ? min(BN / BMQ, nsub) : 0);
-  const int ntail = (!key_edge && (N % BMQ) != 0 && nsub > nlo) ? 1 : 0;
-  const int per_m = nlo + ntail, per_u = nsub - per_m;
-  const int nmasked = G * per_m;
-  // Step order: the masked steps first (per q-head g: the nlo leading
-  // sub-tiles, then the partial tail one), then the unmasked ones (per g).
-  // Positions are walked one step at a time (st, g, jj = index within g), so
-  // no integer division (a long VALU reciprocal sequence) runs per slot.
-  struct StepPos {
-    int st, g, jj;
-  };
-  auto advance = [&](StepPos& s) {
-    ++s.st;
-    ++s.jj;
-    if (s.st == nmasked) {
-      s.g = 0;
-      s.jj = 0;
-    } else if (s.st < nmasked) {
-      if (s.jj == per_m) {
-        s.jj = 0;
-        ++s.g;
-      }
-    } else if (s.jj == per_u) {
-      s.jj = 0;
-      ++s.g;
-    }
-  };
-  auto q0_of = [&](const StepPos& s) {
-    return qstart + BMQ * (s.st < nmasked ? (s.jj < nlo ? s.jj : nsub - 1) : nlo + s.jj);
-  };
-  auto skipped = [&](const StepPos& s) {
-    return s.st < nmasked && (kw >= N || (CAUSAL && q0_of(s) + BMQ - 1 < kw));
-  };
-  auto bufof = [&](int st) { return lds0 + (st & (NB - 1)) * BUF; };
-
-  auto issue = [&](const StepPos& s) {
-    if (s.st >= nsteps) return;
-    const int q0 = q0_of(s);
-    const int hq = hk * G + s.g;
-    const uint32_t buf = bufof(s.st);
-    const char* qg = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + hq * p.q.sh) * 2;
-    const char* dog = static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + hq * p.dout.sh) * 2;
-    if (q0 + BMQ <= N) {
-      tile_load_pieces<D, BMQ, NW, false>(qg, p.q.ss, q0, N, buf, wave, llq);
-      tile_load_pieces<D, BMQ, NW, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
-    } else {
-      tile_load_pieces<D, BMQ, NW, true>(qg, p.q.ss, q0, N, buf, wave, llq);
-      tile_load_pieces<D, BMQ, NW, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
-    }
-    if (wave == NW - 1) {
-      const int64_t rw = sv.mrow(b, hq, p.Hq, p.T, p.N);
-      pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
-    }
-  };
-  StepPos ip{0, 0, 0};  // next step to load
-  issue(ip);
-  // B operands of S^T / dP^T: key l16, columns 32 ks + 8 row16_chunk(g4) .. + 8
-  // (the column order of the Row16Base fetches of Q and dO)
-  v8 kf[KS], vf[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const int col = ks * 32 + 8 * row16_chunk(g4);
-    kf[ks] = key < N ? load16<v8>(kg + key * p.k.ss + col) : zero8<v8>();
-    vf[ks] = key < N ? load16<v8>(vg + key * p.v.ss + col) : zero8<v8>();
-  }
-  wait_vm<0>();  // sub-tile 0 and the K/V fragments
-  for (int st = 1; st < PF; ++st) {
-    advance(ip);
-    issue(ip);
-  }
-  advance(ip);
-  // before slot j reads sub-tile j + 1: the loads of j + 2 .. min(j + PF - 1,
-  // nsteps - 1) may stay in flight (in-order completion of each wave's loads)
-  // With dS' stores (one per slot, also counted by vmcnt) lw - 1 extra
-  // outstanding operations are allowed: if the loads of j + 1 were still in
-  // flight, the (PF - 1) lw loads issued since would exceed that count alone.
-  auto wait_next = [&](int j) {
-    if (j + PF <= nsteps) {
-      if constexpr (DS)
-        wait_vm_slots_slack<PF - 2>(lw);
-      else
-        wait_vm_slots<PF - 2>(lw);
-    } else {
-      wait_vm<0>();
-    }
-  };
-
-  f32x4 dk[DT], dv[DT];
-#pragma unroll
-  for (int i = 0; i < DT; ++i) {
-    dk[i] = f32x4{};
-    dv[i] = f32x4{};
-  }
-  float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;
-  f32x4 sc[2], dc[2], sn[2], dn2[2];  // S^T, dP^T tiles of sub-tiles j and j + 1
-  v8 pa, sa, pa2, sa2;                // P, dS' operands of sub-tiles j - 1 and j
-
-  auto kahan = [&](float tdn, float tdb) {
-    const float y = tdn - dn_c, t = dn_acc + y;
-    dn_c = (t - dn_acc) - y;
-    dn_acc = t;
-    const float y2 = tdb - db_c, t2 = db_acc + y2;
-    db_c = (t2 - db_acc) - y2;
-    db_acc = t2;
-  };
-  auto sdp = [&](int st, f32x4* s_out, f32x4* d_out) {
-    const Row16Base rq = at_tile(rb, bufof(st)), rd = at_tile(rb, bufof(st) + TILE);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s_out[t] = f32x4{};
-      d_out[t] = f32x4{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s_out[t] = mfma16(tile_read_row16<v8>(rq, ks, t), kf[ks], s_out[t]);
-        d_out[t] = mfma16(tile_read_row16<v8>(rd, ks, t), vf[ks], d_out[t]);
-      }
-    }
-  };
-  auto dvdk = [&](int st, const v8& pp, const v8& ss) {
-    const Tr16Base tq = at_tile(tb, bufof(st)), td = at_tile(tb, bufof(st) + TILE);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const v8 dob = __builtin_shufflevector(tile_read_tr16<v4>(td, dt, 0), tile_read_tr16<v4>(td, dt, 1), 0, 1, 2, 3,
-                                             4, 5, 6, 7);
-      const v8 qb = __builtin_shufflevector(tile_read_tr16<v4>(tq, dt, 0), tile_read_tr16<v4>(tq, dt, 1), 0, 1, 2, 3,
-                                            4, 5, 6, 7);
-      dv[dt] = mfma16(pp, dob, dv[dt]);
-      dk[dt] = mfma16(ss, qb, dk[dt]);
-    }
-  };
-  auto elementwise = [&](const StepPos& s, auto masked_tag) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    const int q0 = q0_of(s);
-    const uint32_t ml = bufof(s.st) + 2 * TILE;
-    float tdn = 0.f, tdb = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const f32x4_t mv = lds_read_f4(ml + (16 * t + 4 * g4) * 4);
-      const f32x4_t dv4 = lds_read_f4(ml + 128 + (16 * t + 4 * g4) * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = sc[t][i];
-        const float u1 = fmaf(c, fabsf(x), 1.f);
-        const float sl = copysignf(fast_log2(u1), x);
-        float pv = fast_exp2(fmaf(n, sl, -mv[i]));
-        if (MASKED) {
-          const int qi = q0 + 16 * t + 4 * g4 + i;
-          const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
-          pv = valid ? pv : 0.f;
-        }
-        const float dt = pv * (dc[t][i] - dv4[i]);
-        const float dsp = dt * fast_rcp(u1);
-        tdn = fmaf(dt, sl, tdn);
-        tdb = fmaf(dsp, x, tdb);
-        pa2[4 * t + i] = static_cast<T>(pv);
-        sa2[4 * t + i] = static_cast<T>(dsp);
-      }
-    }
-    kahan(tdn, tdb);
-  };
-  auto rotate = [&]() {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      sc[t] = sn[t];
-      dc[t] = dn2[t];
-    }
-    pa = pa2;
-    sa = sa2;
-  };
-  // dS' of a sub-tile (32 queries x this wave's 16 keys) to its 1 KB workspace
-  // tile exactly as the registers hold it: lane 16 g + kl, key kl, element
-  // 4 t + i = query 16 t + 4 g + i.  The dQ kernel transposes it on its LDS
-  // reads.
-  auto ds_dst = [&](const StepPos& s) {
-    const int q0 = q0_of(s);
-    const int hq = hk * G + s.g;
-    const int64_t tile = (static_cast<int64_t>(b) * p.Hq + hq) * ds_tiles_per_head(N, CAUSAL) +
-                         ds_row_offset(q0 >> 5, N, CAUSAL) + (kw >> 4);
-    return static_cast<T*>(p.ds) + tile * 512 + lane * 8;
-  };
-  auto ds_store = [&](T* dst, const v8& val) { *reinterpret_cast<v8*>(dst) = val; };
-  // positions of sub-tiles j - 1, j, j + 1 (rolled at the end of each slot)
-  StepPos prv{-1, 0, 0}, cur{0, 0, 0}, nxt{0, 0, 0};
-  advance(nxt);
-  auto roll = [&]() {
-    prv = cur;
-    cur = nxt;
-    advance(nxt);
-    advance(ip);
-  };
-  auto slot_generic = [&](int j) {
-    wait_next(j);
-    __builtin_amdgcn_s_barrier();
-    issue(ip);
-    if (j >= 1 && j - 1 < nsteps && !skipped(prv)) dvdk(j - 1, pa, sa);
-    if (j + 1 < nsteps && !skipped(nxt)) sdp(j + 1, sn, dn2);
-    if (j < nsteps && !skipped(cur)) {
-      if (j < nmasked)
-        elementwise(cur, std::true_type{});
-      else
-        elementwise(cur, std::false_type{});
-      if constexpr (DS) ds_store(ds_dst(cur), sa2);
-    }
-    rotate();
-    roll();
-  };
-
-  // steady state: 32 fenced ticks, MFMA g at tick g * 32 / NG with its operand
-  // reads RA MFMAs ahead; element e of S_j runs A at tick 4e - 8, B at 4e - 3,
-  // C1 at 4e + 2, C2 at 4e + 3.
-  auto slot_fast = [&](int j) {
-    constexpr int NG = 2 * DT + 4 * KS;  // dV, dK per column tile; S, dP per row tile and k-step
-    constexpr int STRIDE = 32 / NG;
-    wait_next(j);
-    __builtin_amdgcn_s_barrier();
-    issue(ip);
-    const Tr16Base tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
-    const Row16Base rq = at_tile(rb, bufof(j + 1)), rd = at_tile(rb, bufof(j + 1) + TILE);
-    const uint32_t ml = bufof(j) + 2 * TILE;
-    f32x4_t mq[2], dq4[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      mq[t] = lds_read_f4(ml + (16 * t + 4 * g4) * 4);
-      dq4[t] = lds_read_f4(ml + 128 + (16 * t + 4 * g4) * 4);
-    }
-    // operand reads run RA MFMAs ahead, through a ring of RA + 1 registers
-    constexpr int RA = 4, NO = RA + 1;
-    v8 ops[NO];
-    // MFMA g < 2 DT: dV (even) / dK (odd) for tile dt = g / 2; else S (even) /
-    // dP (odd), h = g - 2 DT: k-step ks = h / 4, row tile t = h / 2 % 2 (each
-    // accumulator's chain of k-steps 4 MFMAs apart).
-    auto read = [&](auto gc) {
-      constexpr int Gi = decltype(gc)::value;
-      if constexpr (Gi < 2 * DT) {
-        constexpr int dt = Gi / 2;
-        const Tr16Base& tr = (Gi % 2 == 0) ? td : tq;
-        ops[Gi % NO] = __builtin_shufflevector(tile_read_tr16<v4>(tr, dt, 0), tile_read_tr16<v4>(tr, dt, 1), 0, 1, 2,
-                                               3, 4, 5, 6, 7);
-      } else if constexpr (Gi < NG) {
-        constexpr int h = Gi - 2 * DT, ks = h / 4, t = (h / 2) % 2;
-        ops[Gi % NO] = tile_read_row16<v8>((h % 2 == 0) ? rq : rd, ks, t);
-      }
-    };
-    auto mfma = [&](auto gc) {
-      constexpr int Gi = decltype(gc)::value;
-      if constexpr (Gi < 2 * DT) {
-        constexpr int dt = Gi / 2;
-        if constexpr (Gi % 2 == 0)
-          dv[dt] = mfma16(pa, ops[Gi % NO], dv[dt]);
-        else
-          dk[dt] = mfma16(sa, ops[Gi % NO], dk[dt]);
-      } else {
-        constexpr int h = Gi - 2 * DT, ks = h / 4, t = (h / 2) % 2;
-        if constexpr (h % 2 == 0)
-          sn[t] = mfma16(ops[Gi % NO], kf[ks], ks == 0 ? f32x4{} : sn[t]);
-        else
-          dn2[t] = mfma16(ops[Gi % NO], vf[ks], ks == 0 ? f32x4{} : dn2[t]);
-      }
-    };
-    float Lv[8], rv[8], slv[8], pv[8], ddv[8], dtv[8], dsv[8];
-    float tdn = 0.f, tdb = 0.f;
-    auto A = [&](int e) {
-      const float x = sc[e >> 2][e & 3];
-      const float u1 = fmaf(c, fabsf(x), 1.f);
-      Lv[e] = fast_log2(u1);
-      rv[e] = fast_rcp(u1);
-      pin(Lv[e]);
-      pin(rv[e]);
-    };
-    auto B = [&](int e) {
-      const float x = sc[e >> 2][e & 3];
-      slv[e] = copysignf(Lv[e], x);
-      pv[e] = fast_exp2(fmaf(n, slv[e], -mq[e >> 2][e & 3]));
-      ddv[e] = dc[e >> 2][e & 3] - dq4[e >> 2][e & 3];
-      pin(pv[e]);
-      pin(ddv[e]);
-    };
-    auto C1 = [&](int e) {
-      dtv[e] = pv[e] * ddv[e];
-      dsv[e] = dtv[e] * rv[e];
-      pin(dtv[e]);
-      pin(dsv[e]);
-    };
-    auto C2 = [&](int e) {
-      tdn = fmaf(dtv[e], slv[e], tdn);
-      tdb = fmaf(dsv[e], sc[e >> 2][e & 3], tdb);
-      pin(tdn);
-      pin(tdb);
-      if (e & 1) {
-        pa2[e - 1] = static_cast<T>(pv[e - 1]);
-        pa2[e] = static_cast<T>(pv[e]);
-        sa2[e - 1] = static_cast<T>(dsv[e - 1]);
-        sa2[e] = static_cast<T>(dsv[e]);
-      }
-    };
-    auto tick = [&](auto tc) {
-      constexpr int t = decltype(tc)::value;
-      if constexpr (t % STRIDE == 0) {
-        read(std::integral_constant<int, t / STRIDE + RA>{});
-        mfma(std::integral_constant<int, t / STRIDE>{});
-      }
-      constexpr int e = t / 4, ph = t % 4;
-      if constexpr (ph == 0) {
-        if constexpr (e + 2 < 8) A(e + 2);
-      } else if constexpr (ph == 1) {
-        if constexpr (e + 1 < 8) B(e + 1);
-      } else if constexpr (ph == 2) {
-        C1(e);
-      } else {
-        C2(e);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    [&]<int... r>(std::integer_sequence<int, r...>) {
-      (read(std::integral_constant<int, r>{}), ...);
-    }(std::make_integer_sequence<int, RA>{});
-    A(0);
-    A(1);
-    B(0);
-    [&]<int... t>(std::integer_sequence<int, t...>) {
-      (tick(std::integral_constant<int, t>{}), ...);
-    }(std::make_integer_sequence<int, 32>{});
-    kahan(tdn, tdb);
-    if constexpr (DS) ds_store(ds_dst(cur), sa2);
-    rotate();
-    roll();
-  };
-
-  __builtin_amdgcn_s_barrier();
-  if (!skipped(cur)) sdp(0, sn, dn2);
-  rotate();
-  int j = 0;
-  for (; j <= nmasked && j <= nsteps; ++j) slot_generic(j);
-  for (; j + 1 < nsteps; ++j) slot_fast(j);
-  for (; j <= nsteps; ++j) slot_generic(j);
-
-  // dK (scaled by scale n b) and dV: lane holds d = 16 dt + l16, keys 4 g4 + i.
-  const float kscale = p.scale * n * *p.b_ptr;
-  T* dkg = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;
-  T* dvg = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kr = kw + 4 * g4 + i;
-      if (kr < N) {
-        dkg[kr * p.dk.ss + dt * 16 + l16] = static_cast<T>(dk[dt][i] * kscale);
-        dvg[kr * p.dv.ss + dt * 16 + l16] = static_cast<T>(dv[dt][i]);
-      }
-    }
-  }
-
-  float pdn = dn_acc - dn_c, pdb = db_acc - db_c;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    pdn += __shfl_xor(pdn, off, 64);
-    pdb += __shfl_xor(pdb, off, 64);
-  }
-  if (lane == 0) {
-    red[0][wave] = pdn;
-    red[1][wave] = pdb;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
-    float sdn = 0.f, sdb = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      sdn += red[0][w];
-      sdb += red[1][w];
-    }
     p.partials[static_cast<int64_t>(bhk) * nkb + kb] = kLn2 * sdn;
     p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = n * p.scale * sdb;
   }
@@ -1208,15 +793,13 @@ hipError_t launch_bwd_preprocess(const BwdParams& p, int dtype, int D, hipStream
   return dtype == 0 ? pre_dt<__bf16>(p, D, s) : pre_dt<_Float16>(p, D, s);
 }
 
-// With a dS' workspace: the 16-key kernel, which also stores dS'.  Without:
-// the 32-key kernel (faster when nothing is stored).
 template <typename T, int D, bool CAUSAL>
 static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
   const int grid = dkdv_key_blocks(p.N) * p.B * p.Hkv;
   if (p.ds != nullptr)
-    hipLaunchKernelGGL((ssa_bwd_dkdv16_kernel<T, D, CAUSAL, true>), dim3(grid), dim3(512), 0, s, p);
+    hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, true>), dim3(grid), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, false>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

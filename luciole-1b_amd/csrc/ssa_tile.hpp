@@ -38,27 +38,22 @@ struct BlockLayout {
 // the 1 KB pieces j = w, w + NW, ... of a tile; piece j covers chunks
 // c = 2 (j % IPB) + half (half = lane / 32) of block j / IPB.  With NW and IPB
 // even, c & 3 = 2 (w & 1) + half for all of them, so the row a lane fetches
-// inside a block, pos ^ swizzle(c & 3), is fixed per lane.  Row strides below
+// inside a block, pos ^ 4 (c & 3), is fixed per lane.  Row strides below
 // 2^24 elements (checked on the host) keep every offset under 2^31.
 //
-// Two row swizzles: 4 (c & 3) for the 32x32 operand fetches (RowBase,
-// TrBase), and 8 (c & 1) for the 16x16 ones (Row16Base, Tr16Base).  Measured
-// on gfx950: the LDS serves each half-wave (32 lanes) of a read together; a
-// 16-byte read is at full rate when the two 16-lane groups of a half-wave
-// apply the same permutation to their 256-byte windows, and an 8-byte
-// transpose read when the two chunks a 16-lane group touches (columns
-// 16 dt .. 16 dt + 15) land on different banks, which 8 (c & 1) gives.
-enum class Swizzle { k32, k16 };
-__device__ __forceinline__ constexpr int row_swizzle(Swizzle sw, int c3) {
-  return sw == Swizzle::k32 ? 4 * c3 : 8 * (c3 & 1);
-}
+// The row swizzle 4 (c & 3) fits the gfx950 LDS as measured: a read is served
+// one half-wave (32 lanes) at a time; a 16-byte read runs at full rate when
+// the two 16-lane groups of a half-wave apply the same permutation to their
+// 256-byte windows (RowBase: both groups read one chunk), and an 8-byte
+// transpose read when the chunks its lanes touch land on different banks
+// (TrBase: four chunks, four swizzles).
 struct LoadLane {
   uint32_t off;   // r * row stride + half * 16, bytes
   uint32_t hoff;  // half * 16, bytes
   int r;          // row within the block
-  __device__ __forceinline__ LoadLane(int lane, int wave, int64_t ss, Swizzle sw = Swizzle::k32) {
+  __device__ __forceinline__ LoadLane(int lane, int wave, int64_t ss) {
     const int pos = lane & 31, half = lane >> 5;
-    r = pos ^ row_swizzle(sw, 2 * (wave & 1) + half);
+    r = pos ^ (4 * (2 * (wave & 1) + half));
     hoff = static_cast<uint32_t>(half * 16);
     off = static_cast<uint32_t>(r * ss * 2) + hoff;
   }
@@ -154,117 +149,12 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Wait until at most K groups of `per_group` direct loads are outstanding
-// (per_group wave-uniform; a scalar branch picks the immediate).
-template <int K>
-__device__ __forceinline__ void wait_vm_slots(int per_group) {
-  switch (per_group) {
-    case 0:
-      break;
-    case 1:
-      wait_vm<K>();
-      break;
-    case 2:
-      wait_vm<2 * K>();
-      break;
-    case 3:
-      wait_vm<3 * K>();
-      break;
-    default:
-      wait_vm<0>();
-      break;
-  }
-}
-
-// As wait_vm_slots, plus per_group - 1 further operations (stores issued
-// between the groups) allowed outstanding: while the oldest group is in
-// flight, the K groups after it already exceed the count.
-template <int K>
-__device__ __forceinline__ void wait_vm_slots_slack(int per_group) {
-  switch (per_group) {
-    case 0:
-      break;
-    case 1:
-      wait_vm<K>();
-      break;
-    case 2:
-      wait_vm<2 * K + 1>();
-      break;
-    case 3:
-      wait_vm<3 * K + 2>();
-      break;
-    default:
-      wait_vm<0>();
-      break;
-  }
-}
-
 // A VGPR copy of x that the compiler cannot re-associate with later
 // arithmetic: per-tile base addresses stay in registers and the operand
 // fetches use their immediate offset fields.
 __device__ __forceinline__ uint32_t opaque(uint32_t x) {
   asm volatile("" : "+v"(x));
   return x;
-}
-
-// ---- operand fetches for 16x16x32 MFMAs from a 32-row block (BlockLayout) ----
-//
-// Tiles read with these are loaded with Swizzle::k16: row r of chunk c sits at
-// position r ^ 8 (c & 1).
-//
-// Row-wise operand (A of an M=16 product, k over the columns): lane
-// (g = lane / 16, i = lane % 16) fetches row 16 t + i of chunk 4 ks + row16_chunk(g),
-// i.e. k-slots 8 g .. 8 g + 7 hold columns 32 ks + 8 row16_chunk(g) ..; the
-// other operand of the product must use the same column order.  The
-// permutation (0, 2, 1, 3) puts chunks of equal parity in each half-wave, so
-// both 16-lane groups of a half-wave apply the same row permutation (full
-// rate).  Address: one per-lane base plus the immediate ks * 2048 + t * 256.
-__device__ __forceinline__ constexpr int row16_chunk(int g) { return 2 * (g & 1) + (g >> 1); }
-struct Row16Base {
-  uint32_t b;
-  __device__ __forceinline__ explicit Row16Base(int lane) {
-    const int c = row16_chunk(lane >> 4), i = lane & 15;
-    b = static_cast<uint32_t>(c * 512 + ((i ^ row_swizzle(Swizzle::k16, c)) << 4));
-  }
-};
-__device__ __forceinline__ Row16Base at_tile(const Row16Base& rb, uint32_t lds) {
-  Row16Base r = rb;
-  r.b = opaque(rb.b + lds);
-  return r;
-}
-template <typename V>
-__device__ __forceinline__ V tile_read_row16(const Row16Base& rb, int ks, int t) {
-  return *(const __attribute__((address_space(3))) V*)(uintptr_t)(rb.b + ks * 2048 + t * 256);
-}
-
-// Transposed operand (B of an N=16 product, k over 32 rows): lane group g
-// receives rows 16 t + 4 g + (0..3) of column 16 dt + i -- k-slots 4 t .. 4 t + 3
-// of the operand whose contraction index q maps to row
-//   q(8 g + 4 t + i) = 16 t + 4 g + i,
-// the row order in which a 16x16 accumulator holds a [32 x 16] block's two
-// row tiles.  Lane i of a group supplies row 16 t + 4 g + i / 4 and columns
-// 16 dt + 4 (i % 4) .. + 3 (8 bytes), chunk c = 2 dt + ch (ch = i % 4 / 2),
-// at position (4 g + i / 4) ^ 8 ch: the two chunks of a group on different
-// banks.
-struct Tr16Base {
-  uint32_t b;
-  __device__ __forceinline__ explicit Tr16Base(int lane) {
-    const int g = lane >> 4, i = lane & 15, ch = (i & 3) >> 1;
-    const int pos = (4 * g + (i >> 2)) ^ row_swizzle(Swizzle::k16, ch);
-    b = static_cast<uint32_t>(ch * 512 + (pos << 4) + ((i & 1) << 3));
-  }
-};
-__device__ __forceinline__ Tr16Base at_tile(const Tr16Base& tb, uint32_t lds) {
-  Tr16Base r = tb;
-  r.b = opaque(tb.b + lds);
-  return r;
-}
-template <typename V4>
-__device__ __forceinline__ V4 tile_read_tr16(const Tr16Base& tb, int dt, int t) {
-  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-  const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-      (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(tb.b + dt * 1024 + t * 256));
-  return __builtin_bit_cast(V4, v);
 }
 
 // Per-lane base offsets for the row-wise operand fetch "row 32*blk + l32,
