@@ -160,5 +160,9 @@ constexpr float kLn2 = 0.69314718055994530942f;
 // Lazy rescaling threshold (log2 units): the running max used for exp2 is only
 // moved when a new row max exceeds it by more than this, so p <= 2^kRescaleTau.
 constexpr float kRescaleTau = 8.0f;
+// The pipelined forward tests instead the sum of each lane's p against this
+// bound: every p is at most that sum, and any finite m with p <= 2^20 keeps
+// the fp32 sums far from overflow while M = m + log2(l) stays exact.
+constexpr float kPsumLimit = 1048576.0f;
 
 }  // namespace ssa

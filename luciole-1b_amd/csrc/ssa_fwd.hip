@@ -16,9 +16,11 @@
 // s = scale * q.k.  Because t2 is monotone in s (increasing for n >= 0,
 // decreasing for n < 0), the row max of t2 is t2 at the row max (or min) of
 // s, so the max is taken on the raw scores and p = exp2(n * sL - m) is a
-// single fma + exp.  The running max moves lazily (kRescaleTau); the stored
-// normaliser M = m + log2(l) is exact either way.  Masks are evaluated only on
-// the diagonal tiles and the sequence-end tile.
+// single fma + exp.  The running max moves lazily (kRescaleTau in the masked
+// iterations, which track the max; kPsumLimit in the pipelined ones, which
+// only bound the sum of p); the stored normaliser M = m + log2(l) is exact
+// either way.  Masks are evaluated only on the diagonal tiles and the
+// sequence-end tile.
 #include <type_traits>
 #include <utility>
 
@@ -267,7 +269,7 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
     const RowBase<D> kr = at_tile(rb, lds0 + ((i + 1) & (NB - 1)) * BUF);
     const TrBase<D> vt = at_tile(tb, lds0 + ((i - 1) & (NB - 1)) * BUF + TILE);
     const float neg_m = -m_run;
-    float z = -INFINITY, psum = 0.f;
+    float psum = 0.f;
     v8 ops[3];
     auto read = [&](auto gc) {
       constexpr int G = decltype(gc)::value;
@@ -282,7 +284,7 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
       }
     };
     // Element pipeline, three stages on different elements per chunk:
-    //   A: u = 1 + c|x|, row extreme, L = log2(u)
+    //   A: u = 1 + c|x|, L = log2(u)
     //   B: t = n copysign(L, x) - m, p = exp2(t)
     //   C: sum and bf16 conversion of p
     // chunk g runs A on elements of chunk g + 2, B on g + 1, C on g.
@@ -291,7 +293,6 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
       constexpr int E = decltype(ec)::value;
       if constexpr (E < 32) {
         const float x = sc[E / 16][E % 16];
-        z = fmaxf(z, NPOS ? x : -x);
         Lv[E] = fast_log2(fmaf(c, fabsf(x), 1.f));
         pin(Lv[E]);
       }
@@ -343,18 +344,31 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
     [&]<int... G>(std::integer_sequence<int, G...>) {
       (chunk(std::integral_constant<int, G>{}), ...);
     }(std::make_integer_sequence<int, NG>{});
-    z = pair_max(z);
-    const float sst = NPOS ? z : -z;
-    const float t2max = n * copysignf(fast_log2(fmaf(c, fabsf(sst), 1.f)), sst);
-    if (__any(t2max > m_run + kRescaleTau)) {  // rare: the running max moves
+    // Every p of this lane is at most its sum, so one test per lane bounds
+    // them all (and catches inf / NaN).  Rare: the running max must move.
+    // The tile's true max then comes from S_i recomputed from K_i (still in
+    // LDS), one 32-key block at a time (register pressure), and P is
+    // recomputed against the new max.
+    if (__any(!(psum <= kPsumLimit))) {
+      const RowBase<D> ki = at_tile(rb, lds0 + (i & (NB - 1)) * BUF);
+      float z = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x16 so = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < ND16; ++ds) so = mfma32(tile_read_row<D, v8>(ki, kb, ds), qf[ds], so);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) z = fmaxf(z, NPOS ? so[r] : -so[r]);
+      }
+      z = pair_max(z);
+      const float sst = NPOS ? z : -z;
+      const float t2max = n * copysignf(fast_log2(fmaf(c, fabsf(sst), 1.f)), sst);
       const float mnew = fmaxf(m_run, t2max);
-      const float alpha = fast_exp2(m_run - mnew);
+      const float alpha = fast_exp2(mnew == -INFINITY ? 0.f : m_run - mnew);
       m_run = mnew;
 #pragma unroll
       for (int d = 0; d < ND32; ++d) acc[d] *= alpha;
       l_run *= alpha;
-      // S_i again, one 32-key block at a time (register pressure)
-      const RowBase<D> ki = at_tile(rb, lds0 + (i & (NB - 1)) * BUF);
       psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
