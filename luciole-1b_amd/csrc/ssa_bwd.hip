@@ -87,9 +87,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const int l32 = lane & 31, hh = lane >> 5;
   const int nkb = dkdv_key_blocks(p.N);
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  // Logical order (kv-head, sequence, key block), as in the forward.
-  const int bhk = L / nkb;
-  const int kb = L % nkb;  // ascending = heaviest first under causal
+  // Logical order (kv-head, sequence), key blocks as in the forward's
+  // dispatch order (ascending = heaviest first under causal).
+  int bhk, kb;
+  dispatch_order(L, gridDim.x / nkb, nkb, bhk, kb);
   const int b = bhk % p.B, hk = bhk / p.B;
   const int G = p.Hq / p.Hkv;
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
@@ -485,8 +486,9 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const int nqb = (p.N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   // Logical order (head, sequence, query block), as in the forward.
-  const int hb = L / nqb;
-  const int qb = nqb - 1 - (L % nqb);
+  int hb, rank;
+  dispatch_order(L, gridDim.x / nqb, nqb, hb, rank);
+  const int qb = nqb - 1 - rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
   const int N = sv.N;
@@ -671,8 +673,9 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const int N = p.N;
   const int nqb = (N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int hb = L / nqb;
-  const int qb = CAUSAL ? nqb - 1 - (L % nqb) : L % nqb;
+  int hb, rank;
+  dispatch_order(L, gridDim.x / nqb, nqb, hb, rank);
+  const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t lds_ds = lds0 + NK * KTILE;

@@ -429,11 +429,12 @@ __global__ __launch_bounds__(512) void ssa_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[4 * 2 * 64 * D * 2];
   const int nqb = (p.N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  // Logical order (head, sequence, query block): each XCD's contiguous range
-  // holds a slice of heads of every sequence (balanced when packed sequences
-  // differ in length) and all blocks of one (sequence, head) share its L2.
-  const int hb = L / nqb;
-  const int qb = nqb - 1 - (L % nqb);  // heaviest (last) query block first
+  // Logical order (head, sequence): each XCD's contiguous range holds a slice
+  // of heads of every sequence (balanced when packed sequences differ in
+  // length); query blocks heaviest (last) first within pairs of heads.
+  int hb, rank;
+  dispatch_order(L, gridDim.x / nqb, nqb, hb, rank);
+  const int qb = nqb - 1 - rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
   if (qb * BM >= sv.N) return;  // packed: past the end of a shorter document
