@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 2
+#define SSA_ABI_VERSION 3
 
 /* Status codes. */
 enum {
@@ -191,6 +191,52 @@ typedef struct {
 
 int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* args, void* stream);
 int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* args, void* stream);
+
+/*
+ * Decode: one new query token per sequence against a KV cache.  Sequence b
+ * attends cache rows 0 .. L_b - 1, L_b = cache_seqlens[b] (a DEVICE int32
+ * array, clamped to [0, capacity] on the device); the caller has already
+ * written the new token's key and value at row L_b - 1.  The result equals
+ * the last row of the causal ssa_fwd over the first L_b rows (out and m; an
+ * empty cache gives out = 0, m = -inf).  q and out are [B, Hq, 1, D] views
+ * (stride_s unused), the caches [B, Hkv, capacity, D] views with the usual
+ * layout rules.  The keys are split into num_splits ranges (0: the library's
+ * choice, ssa_decode_num_splits()); with more than one split the partial
+ * results go through `workspace` and a second kernel combines them in a fixed
+ * order.  No reference counterpart: the reference's generation loop re-runs
+ * the full prefix per token (training/train/train_ssa_triton/generate_triton.py:315-331);
+ * the math is the forward's (ssa_triton_kernel.py:95-122).
+ */
+typedef struct ssa_decode_args {
+  ssa_tensor4 q;        /* [B, Hq, 1, D] */
+  ssa_tensor4 k_cache;  /* [B, Hkv, capacity, D] */
+  ssa_tensor4 v_cache;  /* [B, Hkv, capacity, D] */
+  ssa_tensor4 out;      /* [B, Hq, 1, D], written */
+  float* m;             /* optional (NULL: not written) [B, Hq] contiguous fp32 */
+  const int32_t* cache_seqlens;  /* device, batch entries */
+  const float* ssa_n;
+  const float* ssa_b;
+  int32_t batch, heads_q, heads_kv, capacity, head_dim;
+  int32_t dtype;
+  int32_t num_splits;   /* >= 0; 0 = library choice */
+  float softmax_scale;
+  void* workspace;      /* ssa_decode_workspace_bytes() bytes, 16-byte aligned;
+                           may be NULL when that is 0 (one split) */
+} ssa_decode_args;
+
+/* Key splits ssa_decode uses for num_splits = `requested` (0 = library
+   choice: about 512 workgroups, splits of at least 256 keys); 0 on invalid
+   arguments. */
+int32_t ssa_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
+                              int32_t requested);
+
+/* Workspace bytes of ssa_decode: about (head_dim + 2) fp32 per (batch,
+   q-head, split) when it uses more than one split, else 0; 0 on invalid
+   arguments. */
+int64_t ssa_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
+                                   int32_t head_dim, int32_t requested);
+
+int32_t ssa_decode(const ssa_decode_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,7 +7,7 @@ layer names, re-exported from ``ssa_hip_kernel``), ``ssa_attention`` (the
 attention module of ``ssa_triton_attention``, without Megatron).
 """
 
-from .ssa_attention import SSAAttention  # noqa: F401
+from .ssa_attention import SSAAttention, SSAKVCache  # noqa: F401
 from .ssa_flash_attention import (  # noqa: F401
     SSAFlashAttnFunc,
     SSAFlashAttnVarlenFunc,
@@ -16,6 +16,8 @@ from .ssa_flash_attention import (  # noqa: F401
 )
 from .ssa_hip_kernel import (  # noqa: F401
     ssa_bwd_preprocess,
+    ssa_decode_attention,
+    ssa_decode_num_splits,
     ssa_flash_attn_backward,
     ssa_flash_attn_forward,
     ssa_flash_attn_varlen_backward,

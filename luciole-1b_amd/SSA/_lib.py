@@ -40,9 +40,12 @@ EXPORTED_SYMBOLS = (
     "ssa_bwd_reduce",
     "ssa_varlen_fwd",
     "ssa_varlen_bwd",
+    "ssa_decode_num_splits",
+    "ssa_decode_workspace_bytes",
+    "ssa_decode",
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Tensor4(ctypes.Structure):
@@ -111,6 +114,28 @@ class VarlenBwdArgs(ctypes.Structure):
     _fields_ = [("dense", BwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
 
 
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", Tensor4),
+        ("k_cache", Tensor4),
+        ("v_cache", Tensor4),
+        ("out", Tensor4),
+        ("m", ctypes.c_void_p),
+        ("cache_seqlens", ctypes.c_void_p),
+        ("ssa_n", ctypes.c_void_p),
+        ("ssa_b", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32),
+        ("capacity", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("workspace", ctypes.c_void_p),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -129,10 +154,16 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
-    for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs)):
+    for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs),
+                       ("ssa_decode", DecodeArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
+    i32 = ctypes.c_int32
+    lib.ssa_decode_num_splits.restype = ctypes.c_int32
+    lib.ssa_decode_num_splits.argtypes = [i32, i32, i32, i32, i32]
+    lib.ssa_decode_workspace_bytes.restype = ctypes.c_int64
+    lib.ssa_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
 
 
 def lib() -> ctypes.CDLL:

@@ -17,6 +17,12 @@ in production, ``force_contiguous_qkv``), and the kernel writes its output in
 packed sequences (``packed_seq_params`` with ``cu_seqlens_q`` and
 ``max_seqlen_q``, tensors [T, H, D] or [T, 1, H, D]) run on the varlen path,
 which the reference rejects (:154-156).
+
+Generation: ``SSAKVCache`` + ``SSAAttention.forward_decode`` run one token
+per step against the cached keys and values (the decode kernel), where the
+reference's generation loop re-runs the whole prefix through the forward for
+every token (training/train/train_ssa_triton/generate_triton.py:315-331); the
+result is the same causal attention row.
 """
 
 from __future__ import annotations
@@ -28,6 +34,36 @@ import torch
 from torch import nn
 
 from .ssa_flash_attention import ssa_flash_attention, ssa_flash_attention_varlen
+from .ssa_hip_kernel import ssa_decode_attention
+
+
+class SSAKVCache:
+    """Keys and values of one attention layer for generation.
+
+    ``k`` / ``v`` are ``[B, Hkv, capacity, D]`` (the decode kernel's layout);
+    ``seqlens`` (int32 ``[B]``, on the device) counts the cached tokens of each
+    sequence.  Appends write at each sequence's own length without a host
+    synchronisation; positions past ``capacity`` are clamped to its last row,
+    so the caller sizes the cache for the longest generation.
+    """
+
+    def __init__(self, batch: int, heads_kv: int, capacity: int, head_dim: int, dtype=torch.bfloat16,
+                 device="cuda"):
+        self.k = torch.zeros(batch, heads_kv, capacity, head_dim, dtype=dtype, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.seqlens = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.capacity = capacity
+
+    def append(self, key: torch.Tensor, value: torch.Tensor) -> None:
+        """Append ``T`` new tokens per sequence: key / value ``[B, Hkv, T, D]``."""
+        B, _, T, _ = key.shape
+        pos = self.seqlens.long().unsqueeze(1) + torch.arange(T, device=key.device).unsqueeze(0)
+        pos = pos.clamp_(max=self.capacity - 1)
+        bidx = torch.arange(B, device=key.device).unsqueeze(1).expand(B, T)
+        # advanced indices on dims 0 and 2 -> the indexed view is [B, T, Hkv, D]
+        self.k[bidx, :, pos] = key.transpose(1, 2).to(self.k.dtype)
+        self.v[bidx, :, pos] = value.transpose(1, 2).to(self.v.dtype)
+        self.seqlens += T
 
 
 class SSAAttention(nn.Module):
@@ -102,3 +138,15 @@ class SSAAttention(nn.Module):
             ctx = self.attention_dropout(ctx)
         # the output has the strides of q, i.e. [S, B, H, D] memory order: views only
         return ctx.permute(2, 0, 1, 3).reshape(S, B, -1)
+
+    def forward_decode(self, query, key, value, cache: SSAKVCache):
+        """One generation step.  query [1, B, Hq, D], key/value [1, B, Hkv, D]
+        (the new token) -> context [1, B, Hq * D]; the key and value are
+        appended to ``cache`` first, so the token attends itself and the
+        cached prefix (causal)."""
+        if query.shape[0] != 1:
+            raise ValueError("forward_decode takes one new token per sequence ([1, B, H, D])")
+        n, b = self.get_ssa_params()
+        cache.append(key.permute(1, 2, 0, 3), value.permute(1, 2, 0, 3))
+        ctx = ssa_decode_attention(query[0], cache.k, cache.v, cache.seqlens, self.softmax_scale, n, b)
+        return ctx.reshape(1, query.shape[1], -1)

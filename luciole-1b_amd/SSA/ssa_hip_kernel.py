@@ -348,3 +348,80 @@ def warmup_ssa_triton_kernels(
     dout = torch.randn_like(out)
     ssa_flash_attn_backward(q, k, v, out, dout, m, scale, ssa_n, ssa_b, causal=True)
     torch.cuda.synchronize()
+
+
+def _check_cache_layout(t: torch.Tensor, name: str) -> None:
+    """A KV cache is used in place (a copy per decode step would cost more than
+    the step): its layout must already suit the kernels."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        raise ValueError(f"{name}: last dim must be contiguous and the base 16-byte aligned")
+    for dim in range(3):
+        if t.shape[dim] > 1 and (t.stride(dim) % 8 != 0 or t.stride(dim) < 0):
+            raise ValueError(f"{name}: strides must be non-negative multiples of 8 elements")
+    if t.shape[2] > 1 and t.stride(2) >= _MAX_ROW_STRIDE:
+        raise ValueError(f"{name}: row stride must be below 2**24 elements")
+
+
+def ssa_decode_num_splits(B: int, Hq: int, Hkv: int, capacity: int, num_splits: int = 0) -> int:
+    """Key splits the decode kernel uses (``num_splits`` = 0: its own choice)."""
+    return int(_lib.lib().ssa_decode_num_splits(B, Hq, Hkv, capacity, num_splits))
+
+
+def ssa_decode_attention(q, k_cache, v_cache, cache_seqlens, softmax_scale, ssa_n, ssa_b, num_splits=0,
+                         return_m=False):
+    """One decode step: the newest token of every sequence attends its KV cache.
+
+    ``q`` is ``[B, Hq, D]`` or ``[B, Hq, 1, D]``; ``k_cache`` / ``v_cache`` are
+    ``[B, Hkv, capacity, D]`` (any strides whose last one is 1, used in place);
+    ``cache_seqlens`` holds int32 lengths ``[B]``: sequence b attends cache rows
+    ``0 .. cache_seqlens[b] - 1`` and the newest token's key / value are already
+    at row ``cache_seqlens[b] - 1``.  Returns ``out`` shaped like ``q`` (and
+    ``m [B, Hq]`` fp32 with ``return_m``), equal to the last row of
+    ``ssa_flash_attn_forward(causal=True)`` over the cached prefix.  Lengths are
+    read on the device (clamped to ``[0, capacity]``; an empty cache gives
+    ``out = 0``, ``m = -inf``).  No reference counterpart: the reference's
+    generation loop re-runs the whole prefix per token
+    (training/train/train_ssa_triton/generate_triton.py:315-331).
+    """
+    squeeze = q.dim() == 3
+    q4 = q.unsqueeze(2) if squeeze else q
+    if q4.dim() != 4 or q4.shape[2] != 1:
+        raise ValueError("q must be [B, Hq, D] or [B, Hq, 1, D]")
+    if k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("k_cache / v_cache must be [B, Hkv, capacity, D]")
+    B, Hq, _, D = q4.shape
+    Hkv, cap = k_cache.shape[1], k_cache.shape[2]
+    assert Hq % Hkv == 0, f"Hq={Hq} must be divisible by Hkv={Hkv}"
+    assert _is_pow2(D), f"Head dim D={D} must be a power of two"
+    if tuple(k_cache.shape) != (B, Hkv, cap, D) or tuple(v_cache.shape) != (B, Hkv, cap, D):
+        raise ValueError(f"cache shapes {tuple(k_cache.shape)}/{tuple(v_cache.shape)} do not match q {tuple(q.shape)}")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {q.dtype}: the MI355X SSA kernels take bf16 or fp16")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError("q and the caches must share one dtype")
+    if not (q.is_cuda and k_cache.device == q.device and v_cache.device == q.device):
+        raise ValueError("q and the caches must be on the same GPU device")
+    _check_cache_layout(k_cache, "k_cache")
+    _check_cache_layout(v_cache, "v_cache")
+    q4 = _kernel_layout(q4)
+    lens = torch.as_tensor(cache_seqlens, device=q.device)
+    if lens.shape != (B,):
+        raise ValueError(f"cache_seqlens must have shape ({B},)")
+    lens = lens.to(torch.int32).contiguous()
+    n32 = _scalar(ssa_n, q.device)
+    b32 = _scalar(ssa_b, q.device)
+    out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+    m = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_m else None
+    ws_bytes = int(_lib.lib().ssa_decode_workspace_bytes(B, Hq, Hkv, cap, D, int(num_splits)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
+    args = _lib.DecodeArgs(
+        _t4(q4), _t4(k_cache), _t4(v_cache), _t4(out),
+        m.data_ptr() if m is not None else None, lens.data_ptr(), n32.data_ptr(), b32.data_ptr(),
+        B, Hq, Hkv, cap, D, _DTYPES[q.dtype], int(num_splits), float(softmax_scale),
+        ws.data_ptr() if ws is not None else None,
+    )
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.check(_lib.lib().ssa_decode(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_decode")
+    out = out.squeeze(2) if squeeze else out
+    return (out, m) if return_m else out

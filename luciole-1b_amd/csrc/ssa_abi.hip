@@ -122,6 +122,22 @@ int32_t check_varlen(int32_t docs, int32_t max_seqlen, const int32_t* cu, int32_
 
 int32_t launch_status(hipError_t e) { return e == hipSuccess ? SSA_OK : SSA_ERR_LAUNCH; }
 
+bool decode_shape_ok(int32_t B, int32_t Hq, int32_t Hkv, int32_t cap, int32_t requested) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || cap <= 0 || requested < 0 || Hq % Hkv != 0) return false;
+  // one workgroup per (batch, kv-head, group of 32 q-heads, split): int32 grid
+  const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31) / 32);
+  return units * ((static_cast<int64_t>(cap) + 127) / 128) < (1ll << 30) && static_cast<int64_t>(B) * Hq < (1ll << 30);
+}
+
+// Decode workspace: (m, l) pairs of every (batch, q-head, split) record,
+// padded to 16 bytes, then the records' acc[D].
+int64_t decode_ml_floats(int64_t recs) { return (2 * recs + 3) & ~static_cast<int64_t>(3); }
+int64_t decode_ws_bytes(int32_t B, int32_t Hq, int32_t D, int32_t splits) {
+  if (splits <= 1) return 0;
+  const int64_t recs = static_cast<int64_t>(B) * Hq * splits;
+  return (decode_ml_floats(recs) + recs * D) * 4;
+}
+
 }  // namespace
 
 extern "C" {
@@ -154,6 +170,56 @@ int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen) 
 int64_t ssa_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen, int32_t causal) {
   if (batch <= 0 || heads_q <= 0 || seqlen <= 0) return 0;
   return static_cast<int64_t>(batch) * heads_q * ssa::ds_tiles_per_head(seqlen, causal != 0) * 1024;
+}
+
+int32_t ssa_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
+                              int32_t requested) {
+  if (!decode_shape_ok(batch, heads_q, heads_kv, capacity, requested)) return 0;
+  return ssa::decode_splits(batch, heads_q, heads_kv, capacity, requested);
+}
+
+int64_t ssa_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
+                                   int32_t head_dim, int32_t requested) {
+  if (!decode_shape_ok(batch, heads_q, heads_kv, capacity, requested)) return 0;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return 0;
+  return decode_ws_bytes(batch, heads_q, head_dim,
+                         ssa::decode_splits(batch, heads_q, heads_kv, capacity, requested));
+}
+
+int32_t ssa_decode(const ssa_decode_args* a, void* stream) {
+  if (a == nullptr) return SSA_ERR_NULL_POINTER;
+  if (!decode_shape_ok(a->batch, a->heads_q, a->heads_kv, a->capacity, a->num_splits)) return SSA_ERR_SHAPE;
+  if (a->head_dim != 32 && a->head_dim != 64 && a->head_dim != 128) return SSA_ERR_HEAD_DIM;
+  if (a->dtype != SSA_DTYPE_BF16 && a->dtype != SSA_DTYPE_FP16) return SSA_ERR_DTYPE;
+  SSA_TRY(check_tensor(a->q, true));
+  SSA_TRY(check_tensor(a->k_cache, true));
+  SSA_TRY(check_tensor(a->v_cache, true));
+  SSA_TRY(check_tensor(a->out, true));
+  if (a->cache_seqlens == nullptr || a->ssa_n == nullptr || a->ssa_b == nullptr) return SSA_ERR_NULL_POINTER;
+  ssa::DecodeParams p{};
+  p.splits = ssa::decode_splits(a->batch, a->heads_q, a->heads_kv, a->capacity, a->num_splits);
+  p.split_keys = ssa::decode_split_keys(a->capacity, p.splits);
+  if (p.splits > 1) {
+    if (a->workspace == nullptr) return SSA_ERR_NULL_POINTER;
+    if (!aligned16(a->workspace)) return SSA_ERR_ALIGNMENT;
+    const int64_t recs = static_cast<int64_t>(a->batch) * a->heads_q * p.splits;
+    p.ws_ml = static_cast<float*>(a->workspace);
+    p.ws_acc = p.ws_ml + decode_ml_floats(recs);
+  }
+  p.q = to_t4(a->q);
+  p.k = to_t4(a->k_cache);
+  p.v = to_t4(a->v_cache);
+  p.o = to_t4(a->out);
+  p.m = a->m;
+  p.seqlens = a->cache_seqlens;
+  p.n_ptr = a->ssa_n;
+  p.b_ptr = a->ssa_b;
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.cap = a->capacity;
+  p.scale = a->softmax_scale;
+  return launch_status(ssa::launch_decode(p, a->dtype, a->head_dim, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_fwd(const ssa_fwd_args* a, void* stream) {

@@ -146,6 +146,22 @@ struct BwdParams {
   void* ds;
 };
 
+// Decode against a KV cache: q / o [B, Hq, 1, D] (row stride unused), k / v
+// [B, Hkv, cap, D]; sequence b attends keys [0, seqlens[b]) (clamped to
+// [0, cap]).  With splits > 1 every (b, q-head, split) leaves an unnormalised
+// partial (m, l, acc[D]) in ws_ml / ws_acc for the merge kernel.
+struct DecodeParams {
+  Tensor4 q, k, v, o;
+  float* m;  // optional [B, Hq]
+  const int* seqlens;
+  const float* n_ptr;
+  const float* b_ptr;
+  float* ws_ml;   // [B * Hq * splits][2]
+  float* ws_acc;  // [B * Hq * splits][D]
+  int B, Hq, Hkv, cap, splits, split_keys;
+  float scale;
+};
+
 // The sequence a workgroup works on.  For packed batches the document table
 // is clamped to [0, T] and the length to N, so any table keeps every access
 // inside the token stream.

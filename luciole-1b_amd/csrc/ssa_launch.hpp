@@ -14,6 +14,28 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, bool causal, hi
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
 hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 
+hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t stream);
+
+// Decode key splits.  A split covers decode_split_keys() keys (a multiple of
+// 128, whole 32-key tiles for every wave of a workgroup); the default asks for
+// about 512 workgroups (two per CU) but no split shorter than 256 keys.
+inline int decode_split_keys(int cap, int splits) {
+  const int sk = (cap + splits - 1) / splits;
+  return (sk + 127) / 128 * 128;
+}
+inline int decode_splits(int B, int Hq, int Hkv, int cap, int requested) {
+  int want = requested;
+  if (want <= 0) {
+    const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31) / 32);
+    const int64_t most = (cap + 255) / 256;
+    const int64_t w = (512 + units - 1) / units;
+    want = static_cast<int>(w < most ? w : most);
+    if (want < 1) want = 1;
+  }
+  const int sk = decode_split_keys(cap, want);
+  return (cap + sk - 1) / sk;
+}
+
 // Number of key blocks of the dK/dV kernel (each writes one dn and one db partial).
 __host__ __device__ inline int dkdv_key_blocks(int N) { return (N + 127) / 128; }
 

@@ -26,12 +26,17 @@ reference implementation (the reference asserts ``packed_seq_params is None``,
 ``SSA/ssa_triton_attention.py:154-156``); it is defined here as the
 concatenation of independent dense runs, one per document.
 
+Decode against a KV cache has no reference kernel either (the reference's
+generation loop re-runs the prefix, ``generate_triton.py:315-331``); it is
+defined here as the last row of the causal forward over the cached prefix.
+
 Pinning (tests/test_oracle.py): brute-force pure-Python loops plus central
 finite differences on tiny inputs, torch float64 autograd of an independent
 restatement, n = 0 (cumulative mean), b -> 0 with n b = 1 (softmax attention,
 checked against torch's scaled_dot_product_attention), single-key rows,
 ``M`` against scipy's logsumexp, GQA against repeat_interleave, varlen against
-per-document dense runs, causal prefix independence.
+per-document dense runs, causal prefix independence, decode against the
+last row of the causal forward.
 """
 
 from __future__ import annotations
@@ -184,6 +189,30 @@ def ssa_varlen_forward_backward(q, k, v, dout, cu_seqlens, scale, n, b, causal=T
         res["dn"] += r["dn"]
         res["db"] += r["db"]
     return res
+
+
+def ssa_decode(q, k_cache, v_cache, seqlens, scale, n, b):
+    """One decode step: q [B, Hq, D] (the newest token of each sequence),
+    caches [B, Hkv, cap, D], seqlens [B] (clamped to [0, cap]).  Sequence b's
+    query attends cache rows 0 .. L_b - 1: the single query of a non-causal
+    forward over those rows, which is the last row of the causal forward over
+    the prefix.  Returns (out [B, Hq, D], m [B, Hq]); an empty cache gives
+    out = 0, m = -inf."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k_cache, dtype=np.float64)
+    v = np.asarray(v_cache, dtype=np.float64)
+    bsz, hq, d = q.shape
+    cap = k.shape[2]
+    out = np.zeros((bsz, hq, d))
+    m = np.full((bsz, hq), -np.inf)
+    for i in range(bsz):
+        L = min(max(int(np.asarray(seqlens)[i]), 0), cap)
+        if L == 0:
+            continue
+        o, mm = ssa_forward(q[i : i + 1, :, None], k[i : i + 1, :, :L], v[i : i + 1, :, :L], scale, n, b, causal=False)
+        out[i] = o[0, :, 0]
+        m[i] = mm[0, :, 0]
+    return out, m
 
 
 def causal_pairs(bsz: int, hq: int, n: int, causal: bool = True) -> int:

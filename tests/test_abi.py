@@ -189,3 +189,70 @@ def test_varlen_fwd_validation(field, value, status):
 def test_varlen_null_args():
     assert _lib.lib().ssa_varlen_fwd(None, None) == _lib.SSA_ERR_NULL_POINTER
     assert _lib.lib().ssa_varlen_bwd(None, None) == _lib.SSA_ERR_NULL_POINTER
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,cap,req,splits",
+    [
+        (1, 16, 16, 4096, 0, 16),   # 16 units: 512 / 16 = 32, capped at 4096 / 256 = 16
+        (4, 16, 16, 4096, 0, 8),    # 64 units: 8 splits of 512 keys
+        (64, 16, 16, 4096, 0, 1),   # 1024 units fill the GPU already
+        (1, 16, 16, 100, 0, 1),     # too short to split
+        (1, 8, 8, 1000, 3, 3),      # 3 x 384 keys
+        (1, 8, 8, 1000, 1000, 8),   # at most one split per 128 keys
+        (2, 64, 1, 300, 1, 1),
+    ],
+)
+def test_decode_num_splits(B, Hq, Hkv, cap, req, splits):
+    lib = _lib.lib()
+    assert lib.ssa_decode_num_splits(B, Hq, Hkv, cap, req) == splits
+    ws = lib.ssa_decode_workspace_bytes(B, Hq, Hkv, cap, 128, req)
+    if splits == 1:
+        assert ws == 0
+    else:  # (m, l) and acc[D] per record, fp32, (m, l) block padded to 16 bytes
+        recs = B * Hq * splits
+        assert ws == ((2 * recs + 3) // 4 * 4 + recs * 128) * 4
+
+
+def test_decode_sizes_reject_bad_shapes():
+    lib = _lib.lib()
+    for args in ((0, 8, 8, 64, 0), (1, 8, 3, 64, 0), (1, 8, 8, 0, 0), (1, 8, 8, 64, -1)):
+        assert lib.ssa_decode_num_splits(*args) == 0
+        assert lib.ssa_decode_workspace_bytes(*args[:4], 128, args[4]) == 0
+    assert lib.ssa_decode_workspace_bytes(4, 16, 16, 4096, 96, 0) == 0
+
+
+def _decode_args(**kw):
+    q = _lib.Tensor4(FAKE, 8 * 128, 128, 0)
+    kc = _lib.Tensor4(FAKE, 8 * 4096 * 128, 4096 * 128, 128)
+    a = _lib.DecodeArgs(q, kc, kc, q, None, FAKE, FAKE, FAKE, 4, 8, 8, 4096, 128, _lib.SSA_DTYPE_BF16, 0, 0.088,
+                        FAKE)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "field,value,status",
+    [
+        ("heads_kv", 3, _lib.SSA_ERR_SHAPE),
+        ("capacity", 0, _lib.SSA_ERR_SHAPE),
+        ("num_splits", -2, _lib.SSA_ERR_SHAPE),
+        ("head_dim", 48, _lib.SSA_ERR_HEAD_DIM),
+        ("dtype", 3, _lib.SSA_ERR_DTYPE),
+        ("cache_seqlens", None, _lib.SSA_ERR_NULL_POINTER),
+        ("ssa_b", None, _lib.SSA_ERR_NULL_POINTER),
+        ("workspace", None, _lib.SSA_ERR_NULL_POINTER),   # 4 x 8 heads x 4096 keys needs splits
+        ("workspace", FAKE + 4, _lib.SSA_ERR_ALIGNMENT),
+        ("k_cache", _lib.Tensor4(FAKE, 0, 0, 132), _lib.SSA_ERR_ALIGNMENT),
+        ("v_cache", _lib.Tensor4(None, 0, 0, 128), _lib.SSA_ERR_NULL_POINTER),
+        ("out", _lib.Tensor4(FAKE + 8, 0, 0, 0), _lib.SSA_ERR_ALIGNMENT),
+    ],
+)
+def test_decode_validation(field, value, status):
+    a = _decode_args(**{field: value})
+    assert _lib.lib().ssa_decode(ctypes.byref(a), None) == status
+
+
+def test_decode_null_args():
+    assert _lib.lib().ssa_decode(None, None) == _lib.SSA_ERR_NULL_POINTER

@@ -277,3 +277,32 @@ def test_out_for_delta_only_moves_delta_terms():
     p = np.exp(t - t.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     np.testing.assert_allclose(r["delta"], np.sum(p * (do @ v.swapaxes(-1, -2)), -1), rtol=1e-12, atol=1e-12)
+
+
+def test_decode_is_last_row_of_causal_forward():
+    """The decode oracle against the (pinned) causal forward: sequence b's
+    query, placed as the last row of a random prefix of length L_b, gets the
+    causal forward's last-row output and normaliser; cache rows past L_b
+    (filled with large garbage) are ignored, lengths clamp to the capacity,
+    and an empty cache gives zeros and -inf."""
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, cap, D = 4, 6, 3, 23, 8
+    kc, vc = _rand(rng, B, Hkv, cap, D), _rand(rng, B, Hkv, cap, D)
+    qs = _rand(rng, B, Hq, cap, D)  # full prefixes; the decode query is row L - 1
+    lens = [17, 1, 23, 40]
+    for n_val in (1.5, -3.484375):
+        q_dec = np.stack([qs[i, :, min(lens[i], cap) - 1] for i in range(B)])
+        kg, vg = kc.copy(), vc.copy()
+        for i in range(B):
+            L = min(lens[i], cap)
+            kg[i, :, L:] = 1e3
+            vg[i, :, L:] = -1e3
+        out, m = so.ssa_decode(q_dec, kg, vg, lens, 0.4, n_val, 0.8)
+        for i in range(B):
+            L = min(lens[i], cap)
+            fo, fm = so.ssa_forward(qs[i : i + 1, :, :L], kc[i : i + 1, :, :L], vc[i : i + 1, :, :L], 0.4, n_val, 0.8, True)
+            np.testing.assert_allclose(out[i], fo[0, :, L - 1], rtol=1e-12, atol=1e-12)
+            np.testing.assert_allclose(m[i], fm[0, :, L - 1], rtol=1e-12, atol=1e-12)
+    out, m = so.ssa_decode(q_dec, kc, vc, [0, 0, 5, -3], 0.4, 1.5, 0.8)
+    assert np.all(out[[0, 1, 3]] == 0.0) and np.all(np.isneginf(m[[0, 1, 3]]))
+    assert np.all(np.isfinite(m[2]))
