@@ -57,6 +57,12 @@ CONFIGS = {
 # document lengths uniform in [64, 4096] from random.Random(1234), the last
 # document truncated to fill; H = 16, D = 128, causal inside each document.
 VARLEN_CONFIGS = {"varlen16k": (16384, 16, 16, 128, 64, 4096)}
+# Decode step against a KV cache (no reference kernel: the reference re-runs the
+# prefix per generated token): name: (B, Hq, Hkv, cache length, D).
+DECODE_CONFIGS = {
+    "decode_s4096": (16, 16, 16, 4096, 128),
+    "decode_gqa_d64": (16, 32, 8, 4096, 64),
+}
 
 
 def varlen_lengths(total, lo, hi, seed=1234):
@@ -155,7 +161,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="s4096", choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS))
+    ap.add_argument("--config", default="s4096",
+                    choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS) + sorted(DECODE_CONFIGS))
     ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
@@ -180,6 +187,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.config in VARLEN_CONFIGS:
         return bench_varlen(args, dev)
+    if args.config in DECODE_CONFIGS:
+        return bench_decode(args, dev)
     B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     torch.manual_seed(1234)
@@ -373,6 +382,131 @@ def bench_varlen(args, dev):
                    "pairs": pairs, "alg_gflop_per_step": (flops_fwd + flops_bwd) / 1e9},
         "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
         "fwd_ms": fwd_ms, "fwd_tflops": flops_fwd / (fwd_ms * 1e-3) / 1e12,
+    }))
+
+
+def bench_decode(args, dev):
+    """One decode step (every sequence's newest token against its full KV cache).
+
+    A step is HBM-bound: value = algorithmic bytes (K and V cache rows read,
+    q read, out written) per step time.  Also reported: the causal forward
+    over the whole prefix on the same kernels (what the reference's generation
+    loop runs per token), and the fp64 oracle decode on the host cores.
+    """
+    import torch
+
+    from SSA.ssa_hip_kernel import ssa_decode_attention, ssa_decode_num_splits, ssa_flash_attn_forward
+
+    B, Hq, Hkv, L, D = DECODE_CONFIGS[args.config]
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    torch.manual_seed(1234)
+    q = (torch.randn(B, Hq, D, device=dev) * 0.5).to(dtype)
+    kc = (torch.randn(B, Hkv, L, D, device=dev) * 0.5).to(dtype)
+    vc = (torch.randn(B, Hkv, L, D, device=dev) * 0.5).to(dtype)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    n = torch.tensor(1.5, device=dev)
+    bb = torch.tensor(0.8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    esize = 2
+    alg_bytes = 2 * B * Hkv * L * D * esize + 2 * B * Hq * D * esize
+
+    def step():
+        return ssa_decode_attention(q, kc, vc, lens, scale, n, bb)
+
+    log(f"[bench] config={args.config} B={B} Hq={Hq} Hkv={Hkv} L={L} D={D}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    eager_ms = start.elapsed_time(end) / args.steps
+    # A step is tens of microseconds, below the host's per-call cost, so the
+    # device time comes from a HIP graph of `steps` decode steps (replayed
+    # three times, every replay checked against the eager result).
+    ref = step()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        step()
+    stream.wait_stream(side)
+    with torch.cuda.graph(graph):
+        outs = [step() for _ in range(args.steps)]
+    replays = 3
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, ref) for o in outs), "graph replay differs from the eager decode"
+    end.record(stream)
+    torch.cuda.synchronize()
+    # per-replay timing without the checks
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / (replays * args.steps)
+    gbps = alg_bytes / (ms_step * 1e-3) / 1e9
+    # the reference's per-token work: the causal forward over the whole prefix
+    qf = (torch.randn(B, Hq, L, D, device=dev) * 0.5).to(dtype)
+    for _ in range(2):
+        ssa_flash_attn_forward(qf, kc, vc, scale, n, bb, True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(5):
+        ssa_flash_attn_forward(qf, kc, vc, scale, n, bb, True)
+    end.record(stream)
+    torch.cuda.synchronize()
+    prefix_ms = start.elapsed_time(end) / 5
+    # context for the roofline: a plain device copy (reads and writes COPY_MIB MiB)
+    src = torch.empty(COPY_MIB << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(5):
+        dst.copy_(src)
+    end.record(stream)
+    torch.cuda.synchronize()
+    copy_gbps = 2 * (COPY_MIB << 20) / (start.elapsed_time(end) / 5 * 1e-3) / 1e9
+    del src, dst
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
+        from oracle import ssa_oracle as so
+
+        qn = q[:1].float().cpu().numpy()
+        kn, vn = kc[:1].float().cpu().numpy(), vc[:1].float().cpu().numpy()
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 10.0:
+            so.ssa_decode(qn, kn, vn, [L], scale, 1.5, 0.8)
+            reps += 1
+        per_seq = (time.perf_counter() - t0) / reps
+        cpu = {"value": (alg_bytes / B) / per_seq / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"fp64 numpy oracle decode of 1 of the {B} sequences (all {Hq} heads, {L} keys), "
+                         f"{reps} repetitions in 10 s; value = that sequence's bytes / time"}
+    print(json.dumps({
+        "metric": "SSA decode step, KV-cache GB/s, 1 MI355X",
+        "value": gbps, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step, "eager_ms_per_step": eager_ms, "timing": "HIP graph of `steps` decode steps",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": args.dtype,
+        "data": "synthetic: q / K / V caches = 0.5 N(0,1), seed 1234, n=1.5, b=0.8, every cache full",
+        "config": {"workload": f"SSA decode step ({args.config})", "B": B, "Hq": Hq, "Hkv": Hkv,
+                   "cache_len": L, "D": D, "splits": ssa_decode_num_splits(B, Hq, Hkv, L),
+                   "alg_bytes_per_step": alg_bytes},
+        "roofline": {"kernel": "ssa_decode_kernel (+ merge)", "bound": "hbm", "achieved": gbps,
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gbps / PEAK_HBM_GBPS, "traffic": None},
+        "device_copy_gbps": copy_gbps,
+        "prefix_recompute_ms": prefix_ms,
+        "speedup_vs_prefix_recompute": prefix_ms / ms_step,
+        "cpu_baseline": cpu,
     }))
 
 

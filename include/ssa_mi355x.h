@@ -225,7 +225,7 @@ typedef struct ssa_decode_args {
 } ssa_decode_args;
 
 /* Key splits ssa_decode uses for num_splits = `requested` (0 = library
-   choice: about 512 workgroups, splits of at least 256 keys); 0 on invalid
+   choice: about 256 workgroups, splits of at least 256 keys); 0 on invalid
    arguments. */
 int32_t ssa_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
                               int32_t requested);

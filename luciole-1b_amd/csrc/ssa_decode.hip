@@ -13,7 +13,10 @@
 // q-heads sharing it, key split); one workgroup per unit, NW waves, each wave
 // streaming its own 32-key tiles (tile t of the split goes to wave t % NW)
 // through a private LDS ring of NB tiles filled by direct-to-LDS loads NB - 1
-// tiles ahead, so no barrier is needed until the end.  The GQA group is the
+// tiles ahead, so no barrier is needed until the end.  The stream is bound by
+// the loads each CU keeps in flight: as many waves as 128 KB of rings allow
+// (measured: 4 waves with 2-deep rings move 1.6x the bytes of 2 waves with
+// 4-deep rings at D = 128), and one workgroup per CU.  The GQA group is the
 // MFMA's 32-wide column dimension, so the cache is read once per kv-head:
 //   S^T = K Q^T   (A = 32 keys from LDS, B = Q^T of the group in registers)
 //   O^T += V^T P^T (A = V^T via LDS transpose reads, B = P^T from S^T)
@@ -32,15 +35,16 @@ namespace {
 
 template <int D>
 struct DecodeCfg {
-  static constexpr int NW = D == 128 ? 2 : 4;                      // waves per workgroup
+  static constexpr int NW = D == 128 ? 4 : 8;                      // waves per workgroup
   static constexpr int BLOCK = BlockLayout<D>::BLOCK;             // one 32-row K or V block
   static constexpr int TB = 2 * BLOCK;                            // K block, then V block
   static constexpr int NB = 131072 / (NW * TB);                   // ring depth per wave
   static constexpr int LPT = 2 * BlockLayout<D>::IPB;             // loads per tile
   static constexpr int SMEM = NW * NB * TB;                       // 128 KB
   static constexpr int ACC_LD = D + 1;                            // merge row stride (floats)
+  static constexpr int ML_BYTES = NW * 2 * 32 * 4;                // merge (m, l) per wave and q-head
   static_assert(NB >= 2 && (NB - 1) * LPT < 64, "ring depth");
-  static_assert(1024 + NW * 32 * ACC_LD * 4 <= SMEM, "merge area");
+  static_assert(ML_BYTES + NW * 32 * ACC_LD * 4 <= SMEM, "merge area");
 };
 
 // Rows row0 .. row0 + 31 (clamped to nrows - 1) of a [*, D] matrix with row
@@ -167,8 +171,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, i
   // Merge the waves: (m, l) per q-head and acc[q][d] through LDS, then one
   // thread per (q-head, d) combines them in wave order.
   __syncthreads();
-  float* ml = reinterpret_cast<float*>(smem);            // [NW][2][32]
-  float* accs = reinterpret_cast<float*>(smem + 1024);  // [NW][32][ACC_LD]
+  float* ml = reinterpret_cast<float*>(smem);                  // [NW][2][32]
+  float* accs = reinterpret_cast<float*>(smem + C::ML_BYTES);  // [NW][32][ACC_LD]
   if (hh == 0) {
     ml[(wave * 2 + 0) * 32 + l32] = m_run;
     ml[(wave * 2 + 1) * 32 + l32] = l_tot;

@@ -17,8 +17,9 @@ hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t stream);
 
 // Decode key splits.  A split covers decode_split_keys() keys (a multiple of
-// 128, whole 32-key tiles for every wave of a workgroup); the default asks for
-// about 512 workgroups (two per CU) but no split shorter than 256 keys.
+// 128); the default asks for about 256 workgroups (one per CU: a second
+// round of workgroups costs more than the longer splits save) but no split
+// shorter than 256 keys.
 inline int decode_split_keys(int cap, int splits) {
   const int sk = (cap + splits - 1) / splits;
   return (sk + 127) / 128 * 128;
@@ -28,7 +29,7 @@ inline int decode_splits(int B, int Hq, int Hkv, int cap, int requested) {
   if (want <= 0) {
     const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31) / 32);
     const int64_t most = (cap + 255) / 256;
-    const int64_t w = (512 + units - 1) / units;
+    const int64_t w = (256 + units - 1) / units;
     want = static_cast<int>(w < most ? w : most);
     if (want < 1) want = 1;
   }

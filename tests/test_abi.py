@@ -194,8 +194,9 @@ def test_varlen_null_args():
 @pytest.mark.parametrize(
     "B,Hq,Hkv,cap,req,splits",
     [
-        (1, 16, 16, 4096, 0, 16),   # 16 units: 512 / 16 = 32, capped at 4096 / 256 = 16
-        (4, 16, 16, 4096, 0, 8),    # 64 units: 8 splits of 512 keys
+        (1, 16, 16, 4096, 0, 16),   # 16 units: 256 / 16 = 16 splits of 256 keys
+        (1, 8, 8, 4096, 0, 16),     # 8 units: 32 wanted, capped at 4096 / 256 = 16
+        (4, 16, 16, 4096, 0, 4),    # 64 units: 4 splits of 1024 keys
         (64, 16, 16, 4096, 0, 1),   # 1024 units fill the GPU already
         (1, 16, 16, 100, 0, 1),     # too short to split
         (1, 8, 8, 1000, 3, 3),      # 3 x 384 keys
