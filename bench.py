@@ -59,6 +59,9 @@ CONFIGS = {
 VARLEN_CONFIGS = {"varlen16k": (16384, 16, 16, 128, 64, 4096)}
 # Decode step against a KV cache (no reference kernel: the reference re-runs the
 # prefix per generated token): name: (B, Hq, Hkv, cache length, D).
+# one optimizer step of a 1B Llama-style decoder with
+# SSA attention (SSA/ssa_decoder.py defaults), micro-batch 4 x 4096 tokens.
+TRAIN_CONFIGS = {"train1b": 4}
 DECODE_CONFIGS = {
     "decode_s4096": (16, 16, 16, 4096, 128),
     "decode_gqa_d64": (16, 32, 8, 4096, 64),
@@ -162,7 +165,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="s4096",
-                    choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS) + sorted(DECODE_CONFIGS))
+                    choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS) + sorted(DECODE_CONFIGS) + sorted(TRAIN_CONFIGS))
     ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
@@ -189,6 +192,8 @@ def main():
         return bench_varlen(args, dev)
     if args.config in DECODE_CONFIGS:
         return bench_decode(args, dev)
+    if args.config in TRAIN_CONFIGS:
+        return bench_train(args, dev)
     B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     torch.manual_seed(1234)
@@ -382,6 +387,75 @@ def bench_varlen(args, dev):
                    "pairs": pairs, "alg_gflop_per_step": (flops_fwd + flops_bwd) / 1e9},
         "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
         "fwd_ms": fwd_ms, "fwd_tflops": flops_fwd / (fwd_ms * 1e-3) / 1e12,
+    }))
+
+
+def bench_train(args, dev):
+    """One optimizer step of the 1B SSA decoder (forward, loss, backward, fused
+    AdamW) on uniform-random token ids.  value = tokens per second; model
+    FLOPs = 6 N_params tokens + 14 D pairs per layer (attention, the
+    benchmark's count), reported as a fraction of the bf16 peak (MFU)."""
+    import torch
+
+    from SSA.ssa_decoder import SSADecoder, SSADecoderConfig, train_step
+
+    mbs = TRAIN_CONFIGS[args.config]
+    cfg = SSADecoderConfig()
+    S = cfg.seq_length
+    torch.manual_seed(1234)
+    model = SSADecoder(cfg).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    ids = torch.randint(0, cfg.vocab_size, (mbs, S), device=dev)
+    labels = torch.randint(0, cfg.vocab_size, (mbs, S), device=dev)
+    n_params = sum(p.numel() for p in model.parameters())
+    tokens = mbs * S
+    pairs = mbs * cfg.num_attention_heads * S * (S + 1) // 2
+    flops = 6 * n_params * tokens + 14 * cfg.kv_channels * pairs * cfg.num_layers
+    log(f"[bench] config={args.config} params={n_params / 1e9:.3f}B tokens/step={tokens}")
+    losses = []
+    for _ in range(args.warmup):
+        losses.append(train_step(model, opt, ids, labels))
+    torch.cuda.synchronize()
+    log(f"[bench] timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        losses.append(train_step(model, opt, ids, labels))
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) / args.steps * 1e3
+    # attention's share: the SSA op fwd + bwd of one layer, timed alone
+    from SSA.ssa_hip_kernel import ssa_flash_attn_backward, ssa_flash_attn_forward
+
+    H, D = cfg.num_attention_heads, cfg.kv_channels
+    q = (torch.randn(mbs, H, S, D, device=dev) * 0.5).bfloat16()
+    k, v, do = torch.randn_like(q), torch.randn_like(q), torch.randn_like(q)
+    n, bb = torch.tensor(1.5, device=dev), torch.tensor(0.8, device=dev)
+    for _ in range(2):
+        o, m = ssa_flash_attn_forward(q, k, v, 1 / math.sqrt(D), n, bb, True)
+        ssa_flash_attn_backward(q, k, v, o, do, m, 1 / math.sqrt(D), n, bb, True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(5):
+        o, m = ssa_flash_attn_forward(q, k, v, 1 / math.sqrt(D), n, bb, True)
+        ssa_flash_attn_backward(q, k, v, o, do, m, 1 / math.sqrt(D), n, bb, True)
+    torch.cuda.synchronize()
+    attn_ms = (time.perf_counter() - t1) / 5 * 1e3 * cfg.num_layers
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "1B Llama-style SSA decoder train step, tokens/s, 1 MI355X",
+        "value": tokens / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: uniform-random token ids and labels, seed 1234, random init (std 0.02)",
+        "config": {"workload": "1B decoder train step (train1b): forward, loss, backward, fused AdamW",
+                   "layers": cfg.num_layers, "hidden": cfg.hidden_size, "heads": cfg.num_attention_heads,
+                   "head_dim": cfg.kv_channels, "ffn": cfg.ffn_hidden_size, "vocab": cfg.vocab_size,
+                   "seq_len": S, "micro_batch": mbs, "params": n_params,
+                   "precision": "bf16 autocast (GEMMs, SSA attention), fp32 params / norms / loss / AdamW"},
+        "model_tflops": tflops, "mfu": tflops / PEAK_BF16_TFLOPS,
+        "model_gflop_per_step": flops / 1e9,
+        "ssa_attention_ms_per_step": attn_ms, "ssa_attention_share": attn_ms / ms_step,
+        "loss_first_last": [float(losses[0]), float(losses[-1])],
+        "cpu_baseline": None,
     }))
 
 

@@ -4,7 +4,10 @@ kernels behind the reference's Python operator interface.
 Modules mirror the reference package ``training/train/train_ssa_triton/SSA``:
 ``ssa_flash_attention`` (autograd boundary), ``ssa_triton_kernel`` (launch
 layer names, re-exported from ``ssa_hip_kernel``), ``ssa_attention`` (the
-attention module of ``ssa_triton_attention``, without Megatron).
+attention module of ``ssa_triton_attention``, without Megatron, plus the KV
+cache for decoding); ``ssa_decoder`` is the Llama-style decoder of the
+reference's SSA GPT layer spec (``ssa_triton_layer_specs.py``) for end-to-end
+train steps and cached generation.
 """
 
 from .ssa_attention import SSAAttention, SSAKVCache  # noqa: F401

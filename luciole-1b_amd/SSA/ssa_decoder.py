@@ -1,0 +1,212 @@
+"""A Llama-style decoder with SSA attention, without Megatron or NeMo.
+
+The layer mirrors the reference's SSA GPT layer spec
+(training/train/train_ssa_triton/SSA/ssa_triton_layer_specs.py:96-127):
+input RMSNorm -> fused QKV projection -> RoPE -> SSA core attention
+(``SSAAttention``, the module of ssa_triton_attention.py) -> output
+projection -> residual; pre-MLP RMSNorm -> SwiGLU MLP -> residual.  Tensors
+flow in Megatron's [S, B, hidden] order, the fused QKV weight uses Megatron's
+grouped layout (per query group: G query heads, one key head, one value
+head) and the parameter names follow Megatron's
+(``self_attention.linear_qkv``, ``core_attention.ssa_n_raw``, ``mlp.linear_fc1``
+...), so a state dict maps one to one.
+
+``SSADecoderConfig()`` defaults to the end-to-end configuration of the
+benchmark: 24 layers, hidden 2048, 16 heads x 128, SwiGLU FFN 5632, RMSNorm,
+RoPE, vocab 65536, sequence 4096 (about 1.5 B parameters with an untied output
+layer).  ``train_step`` is one optimizer step under bf16 autocast;
+``generate`` runs the prompt through the dense forward once and then one
+decode step per token against per-layer KV caches (the reference's loop
+re-runs the whole prefix per token, training/train/train_ssa_triton/generate_triton.py:315-331).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .ssa_attention import SSAAttention, SSAKVCache
+
+
+@dataclass
+class SSADecoderConfig:
+    num_layers: int = 24
+    hidden_size: int = 2048
+    num_attention_heads: int = 16
+    num_query_groups: int = 16
+    kv_channels: int = 128
+    ffn_hidden_size: int = 5632
+    vocab_size: int = 65536
+    seq_length: int = 4096
+    rotary_base: float = 10000.0
+    norm_eps: float = 1e-5
+    ssa_n: float = 1.5
+    ssa_b: float = 0.8
+    learnable_ssa: bool = True
+    learnable_b: bool = False
+    init_std: float = 0.02
+
+    def num_parameters(self) -> int:
+        h, f, v = self.hidden_size, self.ffn_hidden_size, self.vocab_size
+        qkv = h * (self.num_attention_heads + 2 * self.num_query_groups) * self.kv_channels
+        proj = self.num_attention_heads * self.kv_channels * h
+        per_layer = qkv + proj + 3 * h * f + 2 * h + (2 if self.learnable_b else 1) * int(self.learnable_ssa)
+        return self.num_layers * per_layer + 2 * v * h + h
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, hidden: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+def rope_tables(positions: torch.Tensor, dim: int, base: float):
+    """cos / sin [S, 1, 1, dim] (fp32) for the rotate-half RoPE of Megatron's
+    default (non-interleaved) rotary embedding."""
+    inv = 1.0 / (base ** (torch.arange(0, dim, 2, device=positions.device, dtype=torch.float32) / dim))
+    ang = positions.float()[:, None] * inv[None, :]
+    emb = torch.cat([ang, ang], dim=-1)[:, None, None, :]
+    return emb.cos(), emb.sin()
+
+
+def apply_rope(x, cos, sin):
+    xf = x.float()
+    x1, x2 = xf.chunk(2, dim=-1)
+    rot = torch.cat([-x2, x1], dim=-1)
+    return (xf * cos + rot * sin).to(x.dtype)
+
+
+class SelfAttention(nn.Module):
+    def __init__(self, cfg: SSADecoderConfig, layer_number: int):
+        super().__init__()
+        self.cfg = cfg
+        self.np, self.ng, self.hn = cfg.num_attention_heads, cfg.num_query_groups, cfg.kv_channels
+        self.linear_qkv = nn.Linear(cfg.hidden_size, (self.np + 2 * self.ng) * self.hn, bias=False)
+        self.core_attention = SSAAttention(self.np, self.ng, self.hn, layer_number=layer_number, ssa_n=cfg.ssa_n,
+                                           ssa_b=cfg.ssa_b, learnable_ssa=cfg.learnable_ssa,
+                                           learnable_b=cfg.learnable_b)
+        self.linear_proj = nn.Linear(self.np * self.hn, cfg.hidden_size, bias=False)
+
+    def _qkv(self, x, cos, sin):
+        S, B = x.shape[0], x.shape[1]
+        g = self.np // self.ng
+        mixed = self.linear_qkv(x).view(S, B, self.ng, (g + 2) * self.hn)
+        q, k, v = torch.split(mixed, [g * self.hn, self.hn, self.hn], dim=-1)
+        q = q.reshape(S, B, self.np, self.hn)
+        return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v
+
+    def forward(self, x, cos, sin, cache: Optional[SSAKVCache] = None):
+        q, k, v = self._qkv(x, cos, sin)
+        if cache is None:
+            ctx = self.core_attention(q, k, v)
+        elif x.shape[0] == 1:
+            ctx = self.core_attention.forward_decode(q, k, v, cache)
+        else:  # prompt: dense causal forward, then the keys and values go to the cache
+            ctx = self.core_attention(q, k, v)
+            cache.append(k.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3))
+        return self.linear_proj(ctx)
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg: SSADecoderConfig):
+        super().__init__()
+        self.linear_fc1 = nn.Linear(cfg.hidden_size, 2 * cfg.ffn_hidden_size, bias=False)  # [gate; up]
+        self.linear_fc2 = nn.Linear(cfg.ffn_hidden_size, cfg.hidden_size, bias=False)
+
+    def forward(self, x):
+        gate, up = self.linear_fc1(x).chunk(2, dim=-1)
+        return self.linear_fc2(F.silu(gate) * up)
+
+
+class TransformerLayer(nn.Module):
+    def __init__(self, cfg: SSADecoderConfig, layer_number: int):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
+        self.self_attention = SelfAttention(cfg, layer_number)
+        self.pre_mlp_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
+        self.mlp = MLP(cfg)
+
+    def forward(self, x, cos, sin, cache=None):
+        x = x + self.self_attention(self.input_layernorm(x), cos, sin, cache)
+        return x + self.mlp(self.pre_mlp_layernorm(x))
+
+
+class SSADecoder(nn.Module):
+    def __init__(self, cfg: SSADecoderConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.embedding = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.layers = nn.ModuleList(TransformerLayer(cfg, i + 1) for i in range(cfg.num_layers))
+        self.final_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
+        self.output_layer = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+        self.reset_parameters()
+
+    @torch.no_grad()
+    def reset_parameters(self):
+        std = self.cfg.init_std
+        out_std = std / math.sqrt(2.0 * self.cfg.num_layers)  # scaled init of the residual outputs
+        for name, p in self.named_parameters():
+            if p.dim() < 2:
+                continue
+            p.normal_(0.0, out_std if name.endswith(("linear_proj.weight", "linear_fc2.weight")) else std)
+
+    def forward(self, input_ids, caches: Optional[List[SSAKVCache]] = None, start_pos: int = 0):
+        """input_ids [B, S] -> logits [S, B, vocab] (Megatron order).  With
+        ``caches`` (one per layer) the tokens are positions start_pos .. and
+        their keys / values are appended to the caches."""
+        S = input_ids.shape[1]
+        x = self.embedding(input_ids.t())  # [S, B, h]
+        pos = torch.arange(start_pos, start_pos + S, device=input_ids.device)
+        cos, sin = rope_tables(pos, self.cfg.kv_channels, self.cfg.rotary_base)
+        for i, layer in enumerate(self.layers):
+            x = layer(x, cos, sin, None if caches is None else caches[i])
+        return self.output_layer(self.final_layernorm(x))
+
+    def loss(self, input_ids, labels):
+        logits = self(input_ids)  # [S, B, V]
+        return F.cross_entropy(logits.float().view(-1, logits.shape[-1]), labels.t().reshape(-1))
+
+    def new_caches(self, batch: int, capacity: int, dtype=torch.bfloat16) -> List[SSAKVCache]:
+        dev = self.embedding.weight.device
+        return [SSAKVCache(batch, self.cfg.num_query_groups, capacity, self.cfg.kv_channels, dtype, dev)
+                for _ in range(self.cfg.num_layers)]
+
+    @torch.no_grad()
+    def generate(self, input_ids, max_new_tokens: int, dtype=torch.bfloat16):
+        """Greedy decoding: the prompt through the dense forward, then one decode
+        step per new token.  Returns (tokens [B, P + max_new_tokens], the
+        logits of every generated position [max_new_tokens, B, vocab])."""
+        B, P = input_ids.shape
+        caches = self.new_caches(B, P + max_new_tokens, dtype)
+        out, steps = input_ids, []
+        with torch.autocast("cuda", dtype=dtype):
+            logits = self(input_ids, caches, 0)[-1]
+            for t in range(max_new_tokens):
+                steps.append(logits.float())
+                nxt = logits.argmax(-1, keepdim=True)
+                out = torch.cat([out, nxt], dim=1)
+                if t + 1 < max_new_tokens:
+                    logits = self(nxt, caches, P + t)[-1]
+        return out, torch.stack(steps)
+
+
+def train_step(model: SSADecoder, optimizer: torch.optim.Optimizer, input_ids, labels, dtype=torch.bfloat16):
+    """One optimizer step: forward and loss under autocast (bf16 GEMMs and SSA
+    attention, fp32 norms, RoPE and loss), backward, AdamW update."""
+    optimizer.zero_grad(set_to_none=True)
+    with torch.autocast("cuda", dtype=dtype):
+        loss = model.loss(input_ids, labels)
+    loss.backward()
+    optimizer.step()
+    return loss.detach()
