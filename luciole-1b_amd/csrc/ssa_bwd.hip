@@ -304,7 +304,11 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   auto slot_fast = [&](int j) {
     constexpr int NG = 4 * ND32 + 2 * ND16;  // MFMAs per slot
     constexpr int STRIDE = 32 / NG;           // ticks per MFMA
-    wait_vm<0>();  // sub-tile j + 1
+    // Sub-tile j + 1 (issued in slot j - 1).  The vector-memory counter also
+    // counts stores, in issue order: slot j - 1 (always a storing slot here,
+    // the fast one or the first unmasked generic one) ended with its four dS'
+    // stores, which may stay in flight.
+    wait_vm<DS ? 4 : 0>();
     __builtin_amdgcn_s_barrier();
     issue(j + 2);
     const TrBase<D> tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
