@@ -683,8 +683,12 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t lds_ds = lds0 + NK * KTILE;
+  // K tiles: row-swizzled for D = 128 (whole-row loads), block-chunk-major otherwise
+  constexpr bool ROWSWZ = D == 128;
   const TrBase<D> tb(lane);
   const LoadLane llk(lane, wave, p.k.ss);
+  const RowSwzTr rtb(lane);
+  const RowSwzLoad rlk(lane, p.k.ss);
 
   const int q0 = qb * BM;
   const int wq0 = q0 + wave * 32;
@@ -716,7 +720,10 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   }
 
   auto issue_k = [&](int t) {
-    tile_load_async<D, BN, 4>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, llk);
+    if constexpr (ROWSWZ)
+      rowswz_load<BN, 4>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, rlk);
+    else
+      tile_load_async<D, BN, 4>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, llk);
   };
   auto issue_ds = [&](int t) {
     const uint32_t dst = lds_ds + (t % NDS) * DSTAGE + wave * 4096;
@@ -740,6 +747,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
     issue_k(t + PFK);
     issue_ds(t + PFD);
     const TrBase<D> tk = at_tile(tb, lds0 + (t % NK) * KTILE);
+    const RowSwzTr rk = at_tile(rtb, lds0 + (t % NK) * KTILE);
     const uint32_t dsl = lds_ds + (t % NDS) * DSTAGE + wave * 4096;
     typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -757,8 +765,14 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
       const int blk = s4 >> 1, ks = s4 & 1;
 #pragma unroll
       for (int db = 0; db < ND32; ++db) {
-        const v4 lo = tile_read_tr<D, v4>(tk, blk, ks, 0, db);
-        const v4 hi = tile_read_tr<D, v4>(tk, blk, ks, 1, db);
+        v4 lo, hi;
+        if constexpr (ROWSWZ) {
+          lo = rowswz_read_tr<v4>(rk, blk, ks, 0, db);
+          hi = rowswz_read_tr<v4>(rk, blk, ks, 1, db);
+        } else {
+          lo = tile_read_tr<D, v4>(tk, blk, ks, 0, db);
+          hi = tile_read_tr<D, v4>(tk, blk, ks, 1, db);
+        }
         dq[db] = mfma32(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), dsv, dq[db]);
       }
     }

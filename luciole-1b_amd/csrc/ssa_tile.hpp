@@ -227,6 +227,86 @@ __device__ __forceinline__ V4 tile_read_tr(const TrBase<D>& tb, int blk, int ks,
   return __builtin_bit_cast(V4, v);
 }
 
+// Row-major tile of D = 128 (256-byte rows) with the 64-byte quarters of
+// row r permuted q -> q ^ (r & 3): chunk c (16 bytes) of row r sits at
+// r * 256 + (c ^ 4 (r & 3)) * 16.  A 1 KB direct load then covers four whole
+// rows with every 4-lane group reading 64 contiguous bytes in lane order
+// (measured on the dS' K pass: 7% faster than the block-chunk-major pieces,
+// which touch 32 rows each; a 16-byte-chunk permutation of the same four
+// rows, which breaks the lane order inside 4-lane groups, gained nothing), and
+// the transpose read of a 16-lane group (4 rows x 32 bytes) lands on four
+// distinct 32-byte bank groups.  For operands read only by transpose reads:
+// 16 rows of one chunk (a row-wise MFMA operand fetch) share 4 bank slots.
+struct RowSwzLoad {
+  uint32_t voff;  // lane's byte offset from a piece's first row
+  int rsub;       // row within the piece (lane / 16)
+  int chunk;      // chunk of that row the lane fetches
+  __device__ __forceinline__ RowSwzLoad(int lane, int64_t ss) {
+    rsub = lane >> 4;
+    chunk = (lane & 15) ^ (4 * rsub);  // rows of a piece start at a multiple of 4: r & 3 = rsub
+    voff = static_cast<uint32_t>(rsub * ss * 2 + chunk * 16);
+  }
+};
+
+// Rows row0 .. row0 + ROWS - 1 (clamped to nrows - 1) of a [*, 128] matrix
+// with row stride `ss` elements into a RowSwz tile at `lds`: piece j (rows
+// 4 j .. 4 j + 3) from wave j % NW.
+template <int ROWS, int NW>
+__device__ __forceinline__ void rowswz_load(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
+                                            const RowSwzLoad& rl) {
+  static_assert(ROWS % (4 * NW) == 0, "whole pieces per wave");
+  constexpr int PER = ROWS / 4 / NW;
+  if (row0 + ROWS <= nrows) {
+    const i32x4_t rs = raw_rsrc(g + static_cast<int64_t>(row0) * ss * 2);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int j = wave + NW * i;
+      dma_buffer16(lds + j * 1024, rs, rl.voff, static_cast<int>(4 * j * ss * 2));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int j = wave + NW * i;
+      int row = row0 + 4 * j + rl.rsub;
+      row = row < nrows ? row : nrows - 1;
+      dma_global16(lds + j * 1024, g + (static_cast<int64_t>(row) * ss + rl.chunk * 8) * 2);
+    }
+  }
+}
+
+// Transpose-read bases of a RowSwz tile, one per 32-column block db: lane i
+// of 16-lane group g supplies row 4 hh + i / 4 (+ the immediate rows, a
+// multiple of 8) and the 8 bytes at columns 32 db + 16 (g & 1) + 4 (i % 4).
+struct RowSwzTr {
+  uint32_t b[4];
+  __device__ __forceinline__ explicit RowSwzTr(int lane) {
+    const int g = lane >> 4, i = lane & 15, hh = lane >> 5;
+    const int r8 = 4 * hh + (i >> 2);  // row & 7; row & 3 = i / 4
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      b[db] = static_cast<uint32_t>(r8 * 256 + (((4 * db + 2 * (g & 1) + ((i & 3) >> 1)) ^ (4 * (i >> 2))) * 16) +
+                                    8 * (i & 1));
+  }
+};
+
+__device__ __forceinline__ RowSwzTr at_tile(const RowSwzTr& t, uint32_t lds) {
+  RowSwzTr r = t;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) r.b[db] = opaque(t.b[db] + lds);
+  return r;
+}
+
+// Column 32 db + l32 of rows 32 blk + 16 ks + 8 hi + 4 hh + (0..3), as
+// tile_read_tr returns it from the block-chunk-major layout.
+template <typename V4>
+__device__ __forceinline__ V4 rowswz_read_tr(const RowSwzTr& t, int blk, int ks, int hi, int db) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  const uint32_t imm = (32 * blk + 16 * ks + 8 * hi) * 256;
+  const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(t.b[db] + imm));
+  return __builtin_bit_cast(V4, v);
+}
+
 // Wait until at most N LDS (and scalar-memory) operations of this wave are
 // outstanding; vmcnt and expcnt left at their maxima.
 template <int N>
