@@ -162,8 +162,10 @@ def cpu_baseline(S, D, causal, budget_s=20.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 50; train1b 5)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default 50: the step time settles after ~30 steps "
+                         "of sustained load; train1b 2)")
     ap.add_argument("--config", default="s4096",
                     choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS) + sorted(DECODE_CONFIGS) + sorted(TRAIN_CONFIGS))
     ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
@@ -173,6 +175,11 @@ def main():
                     help="run each kernel of one step once, then a plain copy of COPY_MIB MiB "
                          "(counter calibration), and exit; for rocprofv3 --pmc runs")
     args = ap.parse_args()
+    train = args.config in TRAIN_CONFIGS
+    if args.steps is None:
+        args.steps = 5 if train else 50
+    if args.warmup is None:
+        args.warmup = 2 if train else 50
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
