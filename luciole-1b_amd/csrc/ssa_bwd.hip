@@ -71,6 +71,27 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_kernel(BwdParams p) {
 // issues vector work.  Sub-tiles (Q, dO, M, Delta) live in four LDS buffers:
 // sub-tile t is loaded in slot t - 2 (its buffer last held t - 4, read for
 // the last time in slot t - 3) and complete at the start of slot t - 1.
+// Step st of a dK/dV workgroup -> (q-head g, sub-tile i), walked one step at a
+// time without divisions: masked sub-tiles of every q-head first (j < per_m:
+// i = j for the nlo diagonal ones, then the partial last sub-tile), then the
+// unmasked ones (i = nlo + j).  Scalar state.
+struct StepWalk {
+  int g, j;
+  bool unmasked;
+  __device__ __forceinline__ explicit StepWalk(int nmasked) : g(0), j(0), unmasked(nmasked == 0) {}
+  __device__ __forceinline__ void next(int per_m, int per_u, int G) {
+    ++j;
+    if (j >= (unmasked ? per_u : per_m)) {
+      j = 0;
+      if (++g >= G) {
+        g = 0;
+        unmasked = true;
+      }
+    }
+  }
+  __device__ __forceinline__ int sub(int nlo, int nsub) const { return unmasked ? nlo + j : (j < nlo ? j : nsub - 1); }
+};
+
 template <typename T, int D, bool CAUSAL, bool DS>
 __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
@@ -147,10 +168,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   };
   auto bufof = [&](int st) { return lds0 + (st & (NB - 1)) * BUF; };
 
-  auto issue = [&](int st) {
+  // walkers at the next step to load (j + 2) and at the current step j
+  StepWalk wi(nmasked), wc(nmasked);
+  auto issue = [&](int st, const StepWalk& w) {
     if (st >= nsteps) return;
-    int g;
-    const int q0 = step_q0(st, g);
+    const int g = w.g;
+    const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
     const int hq = hk * G + g;
     const uint32_t buf = bufof(st);
     const char* qg = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + hq * p.q.sh) * 2;
@@ -167,8 +190,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
     }
   };
-  issue(0);
-  issue(1);
+  issue(0, wi);
+  wi.next(per_m, per_u, G);
+  issue(1, wi);
+  wi.next(per_m, per_u, G);
 
   v8 kf[ND16], vf[ND16];
 #pragma unroll
@@ -270,9 +295,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // 16 ks + 8 + 4 hh + (0..3) (elements 4..7): in the tile format (lane
   // 16 g + kl: key kl, queries 16 t + 4 g + (0..3) at elements 4 t ..) these
   // are four 8-byte pieces, g = hh or 2 + hh, t = ks.
-  auto ds_store = [&](int st) {
-    int g;
-    const int q0 = step_q0(st, g);
+  auto ds_store = [&](const StepWalk& w) {
+    const int g = w.g;
+    const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
     const int hq = hk * G + g;
     const int64_t tile = (static_cast<int64_t>(b) * p.Hq + hq) * ds_tiles_per_head(N, CAUSAL) +
                          ds_row_offset(q0 >> 5, N, CAUSAL) + (k0w >> 4);
@@ -287,7 +312,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   auto slot_generic = [&](int j) {
     wait_vm<0>();  // sub-tile j + 1
     __builtin_amdgcn_s_barrier();
-    issue(j + 2);
+    issue(j + 2, wi);
+    wi.next(per_m, per_u, G);
     if (j >= 1 && !skipped(j - 1)) dvdk(j - 1, pa, sa);
     if (j + 1 < nsteps && !skipped(j + 1)) sdp(j + 1, sn, dn2);
     if (j < nsteps && !skipped(j)) {
@@ -295,8 +321,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         elementwise(j, std::true_type{});
       else
         elementwise(j, std::false_type{});
-      if constexpr (DS) ds_store(j);
+      if constexpr (DS) ds_store(wc);
     }
+    wc.next(per_m, per_u, G);
     rotate();
   };
 
@@ -310,7 +337,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     // stores, which may stay in flight.
     wait_vm<DS ? 4 : 0>();
     __builtin_amdgcn_s_barrier();
-    issue(j + 2);
+    issue(j + 2, wi);
+    wi.next(per_m, per_u, G);
     const TrBase<D> tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
     const RowBase<D> rq = at_tile(rb, bufof(j + 1)), rd = at_tile(rb, bufof(j + 1) + TILE);
     const uint32_t ml = bufof(j) + 2 * TILE;
@@ -418,7 +446,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       (tick(std::integral_constant<int, t>{}), ...);
     }(std::make_integer_sequence<int, 32>{});
     kahan(tdn, tdb);
-    if constexpr (DS) ds_store(j);
+    if constexpr (DS) ds_store(wc);
+    wc.next(per_m, per_u, G);
     rotate();
   };
 
