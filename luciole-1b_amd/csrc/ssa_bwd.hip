@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // Logical order (kv-head, sequence), key blocks as in the forward's
   // dispatch order (ascending = heaviest first under causal).
   int bhk, kb;
-  dispatch_order(L, gridDim.x / nkb, nkb, bhk, kb);
+  dispatch_order(L, gridDim.x / nkb, nkb, p.cu_seqlens ? 1 : kOrderGroup, bhk, kb);
   const int b = bhk % p.B, hk = bhk / p.B;
   const int G = p.Hq / p.Hkv;
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   // Logical order (head, sequence, query block), as in the forward.
   int hb, rank;
-  dispatch_order(L, gridDim.x / nqb, nqb, hb, rank);
+  dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
   const int qb = nqb - 1 - rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
@@ -707,7 +707,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const int nqb = (N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   int hb, rank;
-  dispatch_order(L, gridDim.x / nqb, nqb, hb, rank);
+  dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
   const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const uint32_t lds0 = lds_addr(smem);

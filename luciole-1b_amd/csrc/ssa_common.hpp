@@ -92,18 +92,20 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // Dispatch order of a grid of nhb x nblk workgroups (nhb (sequence, head)
 // pairs, nblk blocks each, block weights falling with rank under a causal
 // mask).  Logical block L maps to (hb, rank), rank 0 the heaviest: groups of
-// kOrderGroup consecutive heads hand out their blocks heaviest first,
-// alternating between the heads of the group.  Each XCD dispatches its range
-// of L in order to whichever CU frees first, so this is longest-processing-
-// time-first list scheduling over a pair of heads, and the workgroups that
-// finish last are light ones.  (One head at a time leaves the heaviest blocks
-// of the last head of a range starting late: up to a sixth of the kernel as
-// idle tail.)  Two heads keep the K/V tiles in flight per XCD within its L2.
+// `group` consecutive hb hand out their blocks heaviest first, alternating
+// between the members of the group.  Each XCD dispatches its range of L in
+// order to whichever CU frees first, so with group = 2 this is
+// longest-processing-time-first list scheduling over a pair of heads, and the
+// workgroups that finish last are light ones (one head at a time leaves the
+// heaviest blocks of the last head of a range starting late: up to a sixth of
+// the kernel as idle tail).  Packed batches use group = 1: there the members
+// of a pair are documents of different lengths, whose block weights the rank
+// does not describe (measured: pairs cost the packed benchmark 15 %).
 constexpr int kOrderGroup = 2;
-__device__ __forceinline__ void dispatch_order(int L, int nhb, int nblk, int& hb, int& rank) {
-  const int g = L / (kOrderGroup * nblk), r = L - g * kOrderGroup * nblk;
-  const int gs = min(kOrderGroup, nhb - g * kOrderGroup);  // >= 1 for L < nhb * nblk
-  hb = g * kOrderGroup + r % gs;
+__device__ __forceinline__ void dispatch_order(int L, int nhb, int nblk, int group, int& hb, int& rank) {
+  const int g = L / (group * nblk), r = L - g * group * nblk;
+  const int gs = min(group, nhb - g * group);  // >= 1 for L < nhb * nblk
+  hb = g * group + r % gs;
   rank = r / gs;
 }
 

@@ -433,7 +433,7 @@ __global__ __launch_bounds__(512) void ssa_fwd_kernel(FwdParams p) {
   // of heads of every sequence (balanced when packed sequences differ in
   // length); query blocks heaviest (last) first within pairs of heads.
   int hb, rank;
-  dispatch_order(L, gridDim.x / nqb, nqb, hb, rank);
+  dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
   const int qb = nqb - 1 - rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
