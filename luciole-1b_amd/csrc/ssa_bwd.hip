@@ -170,14 +170,20 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
 
   // walkers at the next step to load (j + 2) and at the current step j
   StepWalk wi(nmasked), wc(nmasked);
+  // Per-workgroup address bases (q-head hk * G): a slot's loads add only the
+  // q-head and row offsets (a fifth fewer instructions per fast slot).
+  const char* q_head0 = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + static_cast<int64_t>(hk) * G * p.q.sh) * 2;
+  const char* do_head0 =
+      static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + static_cast<int64_t>(hk) * G * p.dout.sh) * 2;
+  const int64_t m_row0 = sv.mrow(b, hk * G, p.Hq, p.T, p.N);
+  const int64_t m_hstride = sv.packed ? p.T : p.N;  // M / Delta rows of consecutive q-heads
   auto issue = [&](int st, const StepWalk& w) {
     if (st >= nsteps) return;
     const int g = w.g;
     const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
-    const int hq = hk * G + g;
     const uint32_t buf = bufof(st);
-    const char* qg = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + hq * p.q.sh) * 2;
-    const char* dog = static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + hq * p.dout.sh) * 2;
+    const char* qg = q_head0 + g * p.q.sh * 2;
+    const char* dog = do_head0 + g * p.dout.sh * 2;
     if (q0 + BMQ <= N) {
       tile_load_pieces<D, BMQ, 4, false>(qg, p.q.ss, q0, N, buf, wave, llq);
       tile_load_pieces<D, BMQ, 4, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
@@ -186,7 +192,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       tile_load_pieces<D, BMQ, 4, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
     }
     if (wave == 3) {
-      const int64_t rw = sv.mrow(b, hq, p.Hq, p.T, p.N);
+      const int64_t rw = m_row0 + g * m_hstride;
       pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
     }
   };
@@ -295,13 +301,14 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // 16 ks + 8 + 4 hh + (0..3) (elements 4..7): in the tile format (lane
   // 16 g + kl: key kl, queries 16 t + 4 g + (0..3) at elements 4 t ..) these
   // are four 8-byte pieces, g = hh or 2 + hh, t = ks.
+  // workspace tile (32 x 16) of q-head hk * G + g, query tile qi, key tile k0w / 16:
+  // (b Hq + hk G + g) tiles_per_head + row_offset(qi) + k0w / 16, 512 elements each
+  const int64_t ds_tph = ds_tiles_per_head(N, CAUSAL);
+  T* const ds_head0 = static_cast<T*>(p.ds) + ((static_cast<int64_t>(b) * p.Hq + hk * G) * ds_tph + (k0w >> 4)) * 512;
+  const uint32_t ds_lane = (l32 >> 4) * 512 + (l32 & 15) * 8;
   auto ds_store = [&](const StepWalk& w) {
-    const int g = w.g;
     const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
-    const int hq = hk * G + g;
-    const int64_t tile = (static_cast<int64_t>(b) * p.Hq + hq) * ds_tiles_per_head(N, CAUSAL) +
-                         ds_row_offset(q0 >> 5, N, CAUSAL) + (k0w >> 4);
-    T* dst = static_cast<T*>(p.ds) + tile * 512 + (l32 >> 4) * 512 + (l32 & 15) * 8;
+    T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       *reinterpret_cast<v4*>(dst + (16 * hh) * 8 + 4 * ks) = __builtin_shufflevector(sa2[ks], sa2[ks], 0, 1, 2, 3);
