@@ -234,20 +234,29 @@ __global__ __launch_bounds__(DecodeCfg<D>::NW * 64) void ssa_decode_kernel(Decod
 }
 
 // One thread per output element d of a (sequence, q-head): combine the split
-// partials in split order, out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// partials in split order, out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),
+// in one pass with the running maximum (each split's loads are independent of
+// the running state, so they can all be in flight at once).
 template <typename T, int D>
 __global__ __launch_bounds__(128) void ssa_decode_merge_kernel(DecodeParams p) {
   const int bh = blockIdx.x, d = threadIdx.x;
   const int b = bh / p.Hq, hq = bh - b * p.Hq;
   const int64_t rec0 = static_cast<int64_t>(bh) * p.splits;
-  float M = -INFINITY;
-  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, p.ws_ml[2 * (rec0 + s)]);
-  float Ls = 0.f, O = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < p.splits; ++s) {
-      const float sc = fast_exp2(p.ws_ml[2 * (rec0 + s)] - M);
-      Ls += p.ws_ml[2 * (rec0 + s) + 1] * sc;
-      if (d < D) O += p.ws_acc[(rec0 + s) * D + d] * sc;
+  float M = -INFINITY, Ls = 0.f, O = 0.f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float ms = p.ws_ml[2 * (rec0 + s)];
+    const float ls = p.ws_ml[2 * (rec0 + s) + 1];
+    const float as = d < D ? p.ws_acc[(rec0 + s) * D + d] : 0.f;
+    if (ms == -INFINITY) continue;  // empty split: l = 0, acc = 0
+    if (ms > M) {
+      const float f = fast_exp2(M - ms);  // 0 while M is still -inf
+      Ls = Ls * f + ls;
+      O = O * f + as;
+      M = ms;
+    } else {
+      const float f = fast_exp2(ms - M);
+      Ls += ls * f;
+      O += as * f;
     }
   }
   const float l_safe = Ls > 0.f ? Ls : 1.f;
