@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 3
+#define SSA_ABI_VERSION 4
 
 /* Status codes. */
 enum {
@@ -95,8 +95,9 @@ typedef struct ssa_bwd_args {
   void* ds_workspace;   /* optional (NULL: dq recomputes the scores), 16-byte
                            aligned, ssa_bwd_ds_workspace_bytes() bytes; when
                            set, dkdv stores dS' there and dq reads it back, so
-                           both steps must get the same pointer.  Ignored for
-                           packed sequences (ssa_varlen_bwd recomputes). */
+                           both steps must get the same pointer.  Packed
+                           sequences (ssa_varlen_bwd) need
+                           ssa_varlen_bwd_ds_workspace_bytes() bytes. */
 } ssa_bwd_args;
 
 /* Library ABI version (SSA_ABI_VERSION). */
@@ -191,6 +192,18 @@ typedef struct {
 
 int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* args, void* stream);
 int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* args, void* stream);
+
+/*
+ * Bytes of the optional dS' workspace of ssa_varlen_bwd (dense.ds_workspace):
+ * document i (first token s, length L) keeps its heads' tiles from slot
+ * s / 32 + i on, a slot holding heads_q * (ceil(max_seqlen / 32) + 1) 1 KB
+ * tiles causal (2 * ceil(max_seqlen / 32) without the mask), so the bound
+ * (total_tokens / 32 + batch) slots holds any table, however its documents
+ * are laid out.  0 for invalid sizes.  No reference counterpart (as
+ * ssa_bwd_ds_workspace_bytes).
+ */
+int64_t ssa_varlen_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t max_seqlen, int32_t total_tokens,
+                                          int32_t causal);
 
 /*
  * Decode: one new query token per sequence against a KV cache.  Sequence b

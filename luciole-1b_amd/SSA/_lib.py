@@ -40,12 +40,13 @@ EXPORTED_SYMBOLS = (
     "ssa_bwd_reduce",
     "ssa_varlen_fwd",
     "ssa_varlen_bwd",
+    "ssa_varlen_bwd_ds_workspace_bytes",
     "ssa_decode_num_splits",
     "ssa_decode_workspace_bytes",
     "ssa_decode",
 )
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class Tensor4(ctypes.Structure):
@@ -149,6 +150,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssa_bwd_partials_count.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
     lib.ssa_bwd_ds_workspace_bytes.restype = ctypes.c_int64
     lib.ssa_bwd_ds_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    lib.ssa_varlen_bwd_ds_workspace_bytes.restype = ctypes.c_int64
+    lib.ssa_varlen_bwd_ds_workspace_bytes.argtypes = [ctypes.c_int32] * 5
     for name, argt in (("ssa_fwd", FwdArgs), ("ssa_bwd", BwdArgs), ("ssa_bwd_preprocess", BwdArgs),
                        ("ssa_bwd_dkdv", BwdArgs), ("ssa_bwd_dq", BwdArgs), ("ssa_bwd_reduce", BwdArgs)):
         fn = getattr(lib, name)

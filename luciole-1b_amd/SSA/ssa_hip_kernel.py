@@ -293,8 +293,9 @@ def ssa_flash_attn_varlen_forward(q, k, v, cu_seqlens, max_seqlen, softmax_scale
 
 
 def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen, softmax_scale, ssa_n, ssa_b,
-                                   causal=True):
-    """Packed-sequence backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors."""
+                                   causal=True, ds=None):
+    """Packed-sequence backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors.
+    ``ds``: keep dS' in a workspace (True / False; None: the ``SSA_BWD_DS`` policy)."""
     cu, docs, T, Hq, Hkv, D, max_seqlen = _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen)
     if tuple(out.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape) or out.dtype != q.dtype:
         raise ValueError("out and dout must have the shape (and out the dtype) of q")
@@ -315,11 +316,15 @@ def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen
                            device=dev, dtype=torch.float32)
     dn = torch.empty((), device=dev, dtype=torch.float32)
     db = torch.empty((), device=dev, dtype=torch.float32)
+    ds_bytes = int(lib.ssa_varlen_bwd_ds_workspace_bytes(docs, Hq, max_seqlen, T, int(bool(causal))))
+    ds_ws = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
+             if ds_bytes > 0 and _use_ds_workspace(ds_bytes, D, ds) else None)
     dense = _lib.BwdArgs(
         _t3(q), _t3(k), _t3(v), _t3(out), _t3(dout), _t3(dq), _t3(dk), _t3(dv),
         m.data_ptr(), delta.data_ptr(), partials.data_ptr(), dn.data_ptr(), db.data_ptr(),
         n32.data_ptr(), b32.data_ptr(),
         docs, Hq, Hkv, max_seqlen, D, _DTYPES[q.dtype], int(bool(causal)), float(softmax_scale),
+        ds_ws.data_ptr() if ds_ws is not None else None,
     )
     args = _lib.VarlenBwdArgs(dense, cu.data_ptr(), T)
     with torch.cuda.device(dev):

@@ -172,6 +172,12 @@ int64_t ssa_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqle
   return static_cast<int64_t>(batch) * heads_q * ssa::ds_tiles_per_head(seqlen, causal != 0) * 1024;
 }
 
+int64_t ssa_varlen_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t max_seqlen, int32_t total_tokens,
+                                          int32_t causal) {
+  if (batch <= 0 || heads_q <= 0 || max_seqlen <= 0 || total_tokens < max_seqlen) return 0;
+  return ssa::ds_packed_tiles(batch, heads_q, total_tokens, max_seqlen, causal != 0) * 1024;
+}
+
 int32_t ssa_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
                               int32_t requested) {
   if (!decode_shape_ok(batch, heads_q, heads_kv, capacity, requested)) return 0;
@@ -249,7 +255,6 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
   p.cu_seqlens = va->cu_seqlens;
   p.T = va->total_tokens;
-  p.ds = nullptr;  // packed batches recompute dQ
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool causal = a->causal != 0;
   // Delta over the whole token stream: one sequence of T rows, [H, T] layout.

@@ -302,9 +302,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // 16 g + kl: key kl, queries 16 t + 4 g + (0..3) at elements 4 t ..) these
   // are four 8-byte pieces, g = hh or 2 + hh, t = ks.
   // workspace tile (32 x 16) of q-head hk * G + g, query tile qi, key tile k0w / 16:
-  // (b Hq + hk G + g) tiles_per_head + row_offset(qi) + k0w / 16, 512 elements each
+  // head_tile(b, hk G) + g tiles_per_head + row_offset(qi) + k0w / 16, 512 elements each
   const int64_t ds_tph = ds_tiles_per_head(N, CAUSAL);
-  T* const ds_head0 = static_cast<T*>(p.ds) + ((static_cast<int64_t>(b) * p.Hq + hk * G) * ds_tph + (k0w >> 4)) * 512;
+  T* const ds_head0 =
+      static_cast<T*>(p.ds) + (ds_head_tile(sv.packed, sv.tok0, b, hk * G, p.Hq, N, p.N, CAUSAL) + (k0w >> 4)) * 512;
   const uint32_t ds_lane = (l32 >> 4) * 512 + (l32 & 15) * 8;
   auto ds_store = [&](const StepWalk& w) {
     const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
@@ -710,13 +711,15 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int N = p.N;
-  const int nqb = (N + BM - 1) / BM;
+  const int nqb = (p.N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   int hb, rank;
   dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
   const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
+  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
+  const int N = sv.N;
+  if (qb * BM >= N) return;  // packed: past the end of a shorter document
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t lds_ds = lds0 + NK * KTILE;
   // K tiles: row-swizzled for D = 128 (whole-row loads), block-chunk-major otherwise
@@ -736,10 +739,10 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const int nkj = wq0 >= N ? 0 : (CAUSAL ? min(2 * (wq0 >> 5) + 2, nk16) : nk16);
   const int kj_max = nkj > 0 ? nkj - 1 : 0;
   // the wave's row of workspace tiles (at most 2 nq32 KB: 32-bit offsets)
-  const i32x4_t ds_rsrc = raw_rsrc(static_cast<const char*>(p.ds) +
-                                   ((static_cast<int64_t>(b) * p.Hq + h) * ds_tiles_per_head(N, CAUSAL) +
-                                    ds_row_offset(min(wq0, N - 1) >> 5, N, CAUSAL)) * 1024);
-  const char* kg = static_cast<const char*>(p.k.ptr) + (static_cast<int64_t>(b) * p.k.sb + hk * p.k.sh) * 2;
+  const i32x4_t ds_rsrc =
+      raw_rsrc(static_cast<const char*>(p.ds) + (ds_head_tile(sv.packed, sv.tok0, b, h, p.Hq, N, p.N, CAUSAL) +
+                                                 ds_row_offset(min(wq0, N - 1) >> 5, N, CAUSAL)) * 1024);
+  const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
   // A stored tile holds, in lane s = 16 g + kl, key kl and queries 16 t + 4 g +
   // (0..3) (elements 4 t ..).  LDS slot 16 g + m receives stored lane
   // 16 g + (m ^ 4 g); the B operand (query L % 32, keys 8 r + 4 hh + e) is then
@@ -817,7 +820,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
 
   const float qscale = p.scale * *p.n_ptr * *p.b_ptr;
   if (qrow < N) {
-    T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + b * p.dq.sb + h * p.dq.sh + qrow * p.dq.ss;
+    T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + qrow * p.dq.ss;
 #pragma unroll
     for (int db = 0; db < ND32; ++db) {
 #pragma unroll

@@ -54,4 +54,28 @@ __host__ __device__ inline int64_t ds_row_offset(int qi, int N, bool causal) {
   return causal ? q * (q + 1) : q * 2 * ((N + 31) / 32);
 }
 
+// Packed batches (longest document Nmax, T tokens): document b, first token
+// s0, length L, owns the tiles from ((s0 / 32) + b) * Hq * ds_slot_tiles(Nmax)
+// on, its heads' ds_tiles_per_head(L) tiles one after another.  That range
+// holds ceil(L / 32) slots of Hq * ds_slot_tiles(Nmax) tiles, at least the
+// Hq triangles (nq (nq + 1) <= nq (nq_max + 1), 2 nq^2 <= nq 2 nq_max), and
+// s0 / 32 + b grows by at least ceil(L / 32) from one document to the next,
+// so documents do not overlap.  For any table clamped to [0, T]
+// (s0 + L <= T), floor(s0 / 32) + ceil(L / 32) <= floor(T / 32) + 1, so every
+// tile lies below (T / 32 + B) slots: ds_packed_tiles().
+__host__ __device__ inline int64_t ds_slot_tiles(int Nmax, bool causal) {
+  const int64_t nq = (Nmax + 31) / 32;
+  return causal ? nq + 1 : 2 * nq;
+}
+__host__ __device__ inline int64_t ds_packed_tiles(int B, int Hq, int T, int Nmax, bool causal) {
+  return (static_cast<int64_t>(T / 32) + B) * Hq * ds_slot_tiles(Nmax, causal);
+}
+// First workspace tile of (sequence b, q-head h): packed (tok0 = s0, N = L)
+// or dense (N = Nmax).
+__host__ __device__ inline int64_t ds_head_tile(bool packed, int64_t tok0, int b, int h, int Hq, int N, int Nmax,
+                                                bool causal) {
+  if (packed) return ((tok0 >> 5) + b) * Hq * ds_slot_tiles(Nmax, causal) + h * ds_tiles_per_head(N, causal);
+  return (static_cast<int64_t>(b) * Hq + h) * ds_tiles_per_head(Nmax, causal);
+}
+
 }  // namespace ssa

@@ -11,6 +11,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from SSA import _lib
@@ -83,6 +84,27 @@ def test_ds_workspace_bytes_headline_and_empty():
     assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 4096, 1) == 4 * 16 * 128 * 129 * 1024
     assert lib.ssa_bwd_ds_workspace_bytes(0, 16, 4096, 1) == 0
     assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 0, 0) == 0
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_varlen_ds_workspace_bytes_holds_every_document(causal):
+    # Packed batches: the workspace must hold every document's per-head
+    # tiles (as the dense size of that document) for any split of T tokens,
+    # including the ones the layout packs worst (many documents just past a
+    # multiple of 32 tokens), and 0 for invalid sizes.
+    lib = _lib.lib()
+    rng = np.random.default_rng(7)
+    tables = [[4096], [33] * 31, [1] * 64, [31, 1] * 20, [100, 513, 7, 260]]
+    tables += [list(rng.integers(1, 700, size=int(rng.integers(1, 40)))) for _ in range(20)]
+    Hq = 6
+    for lens in tables:
+        T, B, nmax = int(sum(lens)), len(lens), int(max(lens))
+        got = lib.ssa_varlen_bwd_ds_workspace_bytes(B, Hq, nmax, T, causal)
+        need = sum(lib.ssa_bwd_ds_workspace_bytes(1, Hq, int(L), causal) for L in lens)
+        assert got >= need, (lens, got, need)
+    assert lib.ssa_varlen_bwd_ds_workspace_bytes(0, Hq, 10, 10, causal) == 0
+    assert lib.ssa_varlen_bwd_ds_workspace_bytes(2, Hq, 10, 9, causal) == 0
+    assert lib.ssa_varlen_bwd_ds_workspace_bytes(2, 0, 10, 20, causal) == 0
 
 
 FAKE = 0x10000  # 16-byte aligned, never dereferenced

@@ -10,6 +10,8 @@ dn / db gated as kernel-level functions of the forward output, as in
 test_gpu_parity.  Also: a one-document stream equals the dense path bitwise,
 the committed golden varlen case, and a malformed table (clamped on the
 device, never read out of bounds) against the oracle on the clamped table.
+Every case runs both backward paths: dQ recomputed from the scores and dQ as
+a product with the dS' workspace written by dK/dV (ds=True).
 """
 
 from __future__ import annotations
@@ -43,7 +45,7 @@ def _inputs(lens, Hq, Hkv, D, dtype, dev, seed=1234, scale=0.5):
     return q, k, v, do, cu
 
 
-def _run(dev, q, k, v, do, cu_host, max_seqlen, causal, n_val=1.5, b_val=0.8, oracle_cu=None):
+def _run(dev, q, k, v, do, cu_host, max_seqlen, causal, n_val=1.5, b_val=0.8, oracle_cu=None, ds=False):
     from SSA.ssa_hip_kernel import ssa_flash_attn_varlen_backward, ssa_flash_attn_varlen_forward
 
     D = q.shape[-1]
@@ -52,7 +54,8 @@ def _run(dev, q, k, v, do, cu_host, max_seqlen, causal, n_val=1.5, b_val=0.8, or
     b = torch.tensor(b_val, device=dev)
     cu = cu_host.to(dev)
     out, m = ssa_flash_attn_varlen_forward(q, k, v, cu, max_seqlen, scale, n, b, causal)
-    dq, dk, dv, dn, db = ssa_flash_attn_varlen_backward(q, k, v, out, do, m, cu, max_seqlen, scale, n, b, causal)
+    dq, dk, dv, dn, db = ssa_flash_attn_varlen_backward(q, k, v, out, do, m, cu, max_seqlen, scale, n, b, causal,
+                                                        ds=ds)
     torch.cuda.synchronize()
     ocu = cu_host.numpy() if oracle_cu is None else np.asarray(oracle_cu)
     ref = so.ssa_varlen_forward_backward(_np64(q), _np64(k), _np64(v), _np64(do), ocu, scale, n_val, b_val, causal)
@@ -78,39 +81,45 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
 @pytest.mark.parametrize("lens,Hq,Hkv,D,causal", CASES)
-def test_varlen_parity(gpu, lens, Hq, Hkv, D, causal):
-    label = f"lens={lens} Hq={Hq} Hkv={Hkv} D={D} causal={int(causal)}"
+def test_varlen_parity(gpu, lens, Hq, Hkv, D, causal, ds):
+    label = f"lens={lens} Hq={Hq} Hkv={Hkv} D={D} causal={int(causal)} ds={int(ds)}"
     print(f"[gpu case] varlen {label}", file=sys.stderr, flush=True)
     q, k, v, do, cu = _inputs(lens, Hq, Hkv, D, torch.bfloat16, gpu)
-    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, max(lens), causal)
+    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, max(lens), causal, ds=ds)
     assert merr < 1e-2, f"{label}: m {merr}"
     assert_parity(res, label)
     assert_parity(res_k, label + " [kernel-level]")
 
 
-def test_varlen_fp16(gpu):
+@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
+def test_varlen_fp16(gpu, ds):
+    print(f"[gpu case] varlen fp16 ds={int(ds)}", file=sys.stderr, flush=True)
     q, k, v, do, cu = _inputs((50, 200, 77), 4, 2, 64, torch.float16, gpu)
-    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, 200, True)
+    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, 200, True, ds=ds)
     assert merr < 1e-2
     assert_parity(res, "varlen fp16")
     assert_parity(res_k, "varlen fp16 [kernel-level]")
 
 
-def test_varlen_one_document_equals_dense_bitwise(gpu):
+@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
+def test_varlen_one_document_equals_dense_bitwise(gpu, ds):
     from SSA.ssa_hip_kernel import (ssa_flash_attn_backward, ssa_flash_attn_forward,
                                     ssa_flash_attn_varlen_backward, ssa_flash_attn_varlen_forward)
 
+    print(f"[gpu case] varlen one document ds={int(ds)}", file=sys.stderr, flush=True)
     q, k, v, do, cu = _inputs((333,), 4, 2, 128, torch.bfloat16, gpu)
     n = torch.tensor(1.5, device=gpu)
     b = torch.tensor(0.8, device=gpu)
     s = 1.0 / math.sqrt(128)
     out_v, m_v = ssa_flash_attn_varlen_forward(q, k, v, cu.to(gpu), 333, s, n, b, True)
-    g_v = ssa_flash_attn_varlen_backward(q, k, v, out_v, do, m_v, cu.to(gpu), 333, s, n, b, True)
+    g_v = ssa_flash_attn_varlen_backward(q, k, v, out_v, do, m_v, cu.to(gpu), 333, s, n, b, True, ds=ds)
     dense = lambda t: t.permute(1, 0, 2).unsqueeze(0)  # [T, H, D] -> [1, H, T, D] view
     out_d, m_d = ssa_flash_attn_forward(dense(q), dense(k), dense(v), s, n, b, True)
-    # packed batches always recompute dQ: compare with the dense recompute path
-    g_d = ssa_flash_attn_backward(dense(q), dense(k), dense(v), out_d, dense(do), m_d, s, n, b, True, ds=False)
+    # the same backward path on the dense batch (the workspace layouts differ,
+    # the tiles in them and every product do not)
+    g_d = ssa_flash_attn_backward(dense(q), dense(k), dense(v), out_d, dense(do), m_d, s, n, b, True, ds=ds)
     torch.cuda.synchronize()
     assert torch.equal(out_v, out_d[0].permute(1, 0, 2))
     assert torch.equal(m_v, m_d[0])
@@ -119,7 +128,9 @@ def test_varlen_one_document_equals_dense_bitwise(gpu):
     assert torch.equal(g_v[3], g_d[3]) and torch.equal(g_v[4], g_d[4])
 
 
-def test_varlen_golden(gpu):
+@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
+def test_varlen_golden(gpu, ds):
+    print(f"[gpu case] varlen golden ds={int(ds)}", file=sys.stderr, flush=True)
     z = np.load(Path(__file__).resolve().parent / "golden" / "ssa_golden.npz")
     name = "varlen_d64"
 
@@ -131,7 +142,7 @@ def test_varlen_golden(gpu):
     n_val, b_val, _ = (float(x) for x in z[f"{name}/params"])
     causal = bool(z[f"{name}/meta"][4])
     out, m, (dq, dk, dv, dn, db), res, res_k, merr = _run(gpu, q, k, v, do, cu, int(np.diff(cu.numpy()).max()),
-                                                          causal, n_val, b_val)
+                                                          causal, n_val, b_val, ds=ds)
     assert merr < 1e-2
     assert_parity(res, "golden varlen (live oracle)")
     assert_parity(res_k, "golden varlen [kernel-level]")
@@ -139,11 +150,13 @@ def test_varlen_golden(gpu):
     assert_parity(compare({"out": out, "dq": dq, "dk": dk, "dv": dv}, stored, scalars=()), "golden varlen (fixture)")
 
 
-def test_varlen_malformed_table_is_clamped(gpu):
+@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
+def test_varlen_malformed_table_is_clamped(gpu, ds):
     # cu = [-5, 40, 250] over T = 100 tokens: clamped on the device to the
     # documents [0, 40) and [40, 100) (a negative start, an end past T).
+    print(f"[gpu case] varlen clamped table ds={int(ds)}", file=sys.stderr, flush=True)
     q, k, v, do, _ = _inputs((100,), 2, 2, 64, torch.bfloat16, gpu)
     cu = torch.tensor([-5, 40, 250], dtype=torch.int32)
-    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, 100, True, oracle_cu=[0, 40, 100])
+    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, 100, True, oracle_cu=[0, 40, 100], ds=ds)
     assert merr < 1e-2
     assert_parity(res, "clamped table")
