@@ -307,15 +307,17 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   T* const ds_head0 =
       static_cast<T*>(p.ds) + (ds_head_tile(sv.packed, sv.tok0, b, hk * G, p.Hq, N, p.N, CAUSAL) + (k0w >> 4)) * 512;
   const uint32_t ds_lane = (l32 >> 4) * 512 + (l32 & 15) * 8;
+  // Exactly four vector-memory instructions (the fast slot's load wait
+  // counts them): piece (g, t) at byte 256 g + 8 t of the lane's slot, so
+  // from 256 hh: +0, +8 (g = hh), +512, +520 (g = 2 + hh).
   auto ds_store = [&](const StepWalk& w) {
     const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
-    T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      *reinterpret_cast<v4*>(dst + (16 * hh) * 8 + 4 * ks) = __builtin_shufflevector(sa2[ks], sa2[ks], 0, 1, 2, 3);
-      *reinterpret_cast<v4*>(dst + (16 * (2 + hh)) * 8 + 4 * ks) =
-          __builtin_shufflevector(sa2[ks], sa2[ks], 4, 5, 6, 7);
-    }
+    T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane + (16 * hh) * 8;
+    const u32x4 s0 = __builtin_bit_cast(u32x4, sa2[0]), s1 = __builtin_bit_cast(u32x4, sa2[1]);
+    store_b64<0>(dst, u32x2{s0[0], s0[1]});
+    store_b64<8>(dst, u32x2{s1[0], s1[1]});
+    store_b64<512>(dst, u32x2{s0[2], s0[3]});
+    store_b64<520>(dst, u32x2{s1[2], s1[3]});
   };
   auto slot_generic = [&](int j) {
     wait_vm<0>();  // sub-tile j + 1

@@ -105,6 +105,15 @@ __device__ __forceinline__ void dma_global4(uint32_t lds, const void* src) {
                : "memory", "m0");
 }
 
+// 8 bytes to global memory at p + OFF bytes: exactly one vector-memory
+// instruction, never merged with a neighbour, so a kernel can count its
+// stores for a vmcnt wait.  8-byte data has no store-data hazard.
+template <int OFF>
+__device__ __forceinline__ void store_b64(void* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off offset:%2" : : "v"(reinterpret_cast<uint64_t>(p)), "v"(v), "i"(OFF)
+               : "memory");
+}
+
 template <int D, int ROWS, int NW, bool CLAMP>
 __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
                                                  const LoadLane& ll) {
