@@ -92,7 +92,11 @@ struct StepWalk {
   __device__ __forceinline__ int sub(int nlo, int nsub) const { return unmasked ? nlo + j : (j < nlo ? j : nsub - 1); }
 };
 
-template <typename T, int D, bool CAUSAL, bool DS>
+// OFF32: every Q / dO row a workgroup reads lies below 2 GiB of its base
+// (q-head hk G of the sequence), and so does its dS' range (checked on the
+// host): the per-slot loads and stores then take 32-bit scalar offsets into
+// loop-invariant buffer descriptors instead of 64-bit address arithmetic.
+template <typename T, int D, bool CAUSAL, bool DS, bool OFF32>
 __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
@@ -177,6 +181,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + static_cast<int64_t>(hk) * G * p.dout.sh) * 2;
   const int64_t m_row0 = sv.mrow(b, hk * G, p.Hq, p.T, p.N);
   const int64_t m_hstride = sv.packed ? p.T : p.N;  // M / Delta rows of consecutive q-heads
+  const i32x4_t q_rs = raw_rsrc(q_head0), do_rs = raw_rsrc(do_head0);
+  const int q_hs2 = static_cast<int>(p.q.sh * 2), q_ss2 = static_cast<int>(p.q.ss * 2);
+  const int do_hs2 = static_cast<int>(p.dout.sh * 2), do_ss2 = static_cast<int>(p.dout.ss * 2);
   auto issue = [&](int st, const StepWalk& w) {
     if (st >= nsteps) return;
     const int g = w.g;
@@ -185,8 +192,13 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const char* qg = q_head0 + g * p.q.sh * 2;
     const char* dog = do_head0 + g * p.dout.sh * 2;
     if (q0 + BMQ <= N) {
-      tile_load_pieces<D, BMQ, 4, false>(qg, p.q.ss, q0, N, buf, wave, llq);
-      tile_load_pieces<D, BMQ, 4, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
+      if constexpr (OFF32) {
+        tile_load_pieces_off<D, BMQ, 4>(q_rs, g * q_hs2 + q0 * q_ss2, q_ss2, buf, wave, llq);
+        tile_load_pieces_off<D, BMQ, 4>(do_rs, g * do_hs2 + q0 * do_ss2, do_ss2, buf + TILE, wave, lld);
+      } else {
+        tile_load_pieces<D, BMQ, 4, false>(qg, p.q.ss, q0, N, buf, wave, llq);
+        tile_load_pieces<D, BMQ, 4, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
+      }
     } else {
       tile_load_pieces<D, BMQ, 4, true>(qg, p.q.ss, q0, N, buf, wave, llq);
       tile_load_pieces<D, BMQ, 4, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
@@ -310,14 +322,27 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // Exactly four vector-memory instructions (the fast slot's load wait
   // counts them): piece (g, t) at byte 256 g + 8 t of the lane's slot, so
   // from 256 hh: +0, +8 (g = hh), +512, +520 (g = 2 + hh).
+  const i32x4_t ds_rs = raw_rsrc(ds_head0);
+  const uint32_t ds_voff = (ds_lane + (16 * hh) * 8) * 2;
+  const int ds_tph1k = static_cast<int>(ds_tph * 1024);
   auto ds_store = [&](const StepWalk& w) {
     const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
-    T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane + (16 * hh) * 8;
     const u32x4 s0 = __builtin_bit_cast(u32x4, sa2[0]), s1 = __builtin_bit_cast(u32x4, sa2[1]);
-    store_b64<0>(dst, u32x2{s0[0], s0[1]});
-    store_b64<8>(dst, u32x2{s1[0], s1[1]});
-    store_b64<512>(dst, u32x2{s0[2], s0[3]});
-    store_b64<520>(dst, u32x2{s1[2], s1[3]});
+    if constexpr (OFF32) {
+      const int qi = q0 >> 5;
+      const int soff = __builtin_amdgcn_readfirstlane(w.g * ds_tph1k +
+                                                      (CAUSAL ? qi * (qi + 1) : qi * 2 * ((N + 31) >> 5)) * 1024);
+      buffer_store_b64<0>(ds_rs, ds_voff, soff, u32x2{s0[0], s0[1]});
+      buffer_store_b64<8>(ds_rs, ds_voff, soff, u32x2{s1[0], s1[1]});
+      buffer_store_b64<512>(ds_rs, ds_voff, soff, u32x2{s0[2], s0[3]});
+      buffer_store_b64<520>(ds_rs, ds_voff, soff, u32x2{s1[2], s1[3]});
+    } else {
+      T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane + (16 * hh) * 8;
+      store_b64<0>(dst, u32x2{s0[0], s0[1]});
+      store_b64<8>(dst, u32x2{s1[0], s1[1]});
+      store_b64<512>(dst, u32x2{s0[2], s0[3]});
+      store_b64<520>(dst, u32x2{s1[2], s1[3]});
+    }
   };
   auto slot_generic = [&](int j) {
     wait_vm<0>();  // sub-tile j + 1
@@ -855,13 +880,32 @@ hipError_t launch_bwd_preprocess(const BwdParams& p, int dtype, int D, hipStream
   return dtype == 0 ? pre_dt<__bf16>(p, D, s) : pre_dt<_Float16>(p, D, s);
 }
 
+// Whether every dK/dV workgroup's Q / dO rows (from q-head hk G of its
+// sequence: G heads, N rows, D columns) and its dS' tiles (G triangles of
+// the longest sequence) lie below 2 GiB of their bases; strides are
+// non-negative (validated at the boundary).
+static bool dkdv_off32(const BwdParams& p, int D, bool causal) {
+  const int64_t G = p.Hq / p.Hkv, lim = (int64_t{1} << 31) - 4096;
+  auto span = [&](const Tensor4& t) { return ((G - 1) * t.sh + static_cast<int64_t>(p.N - 1) * t.ss + D) * 2; };
+  if (span(p.q) >= lim || span(p.dout) >= lim) return false;
+  return p.ds == nullptr || G * ds_tiles_per_head(p.N, causal) * 1024 < lim;
+}
+
 template <typename T, int D, bool CAUSAL>
 static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
   const int grid = dkdv_key_blocks(p.N) * p.B * p.Hkv;
-  if (p.ds != nullptr)
-    hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, true>), dim3(grid), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, false>), dim3(grid), dim3(256), 0, s, p);
+  const bool o32 = dkdv_off32(p, D, CAUSAL);
+  if (p.ds != nullptr) {
+    if (o32)
+      hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, true, true>), dim3(grid), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, true, false>), dim3(grid), dim3(256), 0, s, p);
+  } else {
+    if (o32)
+      hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, false, true>), dim3(grid), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, false, false>), dim3(grid), dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 

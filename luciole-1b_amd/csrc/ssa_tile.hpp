@@ -114,6 +114,15 @@ __device__ __forceinline__ void store_b64(void* p, u32x2 v) {
                : "memory");
 }
 
+// 8 bytes to rs.base + voff + soff + OFF: one vector-memory instruction.
+template <int OFF>
+__device__ __forceinline__ void buffer_store_b64(const i32x4_t& rs, uint32_t voff, int soff, u32x2 v) {
+  asm volatile("buffer_store_dwordx2 %0, %1, %2, %3 offen offset:%4"
+               :
+               : "v"(v), "v"(voff), "s"(rs), "s"(soff), "i"(OFF)
+               : "memory");
+}
+
 template <int D, int ROWS, int NW, bool CLAMP>
 __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
                                                  const LoadLane& ll) {
@@ -135,6 +144,26 @@ __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int 
       grow = grow < nrows ? grow : nrows - 1;
       dma_global16(lds + j * 1024, g + (static_cast<int64_t>(grow) * ss + cp * 16) * 2 + ll.hoff);
     }
+  }
+}
+
+// tile_load_pieces for a tile of full rows at byte soff0 of the buffer rs,
+// with 32-bit offsets (the caller keeps every byte of the tile below 2 GiB of
+// the descriptor base): one scalar add per piece, no 64-bit address math.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void tile_load_pieces_off(const i32x4_t& rs, int soff0, int ss2, uint32_t lds, int wave,
+                                                     const LoadLane& ll) {
+  using BL = BlockLayout<D>;
+  constexpr int NINST = ROWS / 32 * BL::IPB;
+  constexpr int PER = (NINST + NW - 1) / NW;
+  // wave-uniform by construction; stated so that the offset is an SGPR
+  const int base = __builtin_amdgcn_readfirstlane(soff0);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = wave + NW * i;
+    if (NINST % NW != 0 && j >= NINST) break;
+    const int blk = j / BL::IPB, cp = j % BL::IPB;
+    dma_buffer16(lds + j * 1024, rs, ll.off, base + blk * 32 * ss2 + cp * 32);
   }
 }
 
