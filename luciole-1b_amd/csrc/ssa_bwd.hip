@@ -90,6 +90,15 @@ struct StepWalk {
     }
   }
   __device__ __forceinline__ int sub(int nlo, int nsub) const { return unmasked ? nlo + j : (j < nlo ? j : nsub - 1); }
+  // The same two inside the unmasked steps (the fast slots walk only those;
+  // past the last step g runs to G, which no step reads).
+  __device__ __forceinline__ void next_unmasked(int per_u) {
+    if (++j >= per_u) {
+      j = 0;
+      ++g;
+    }
+  }
+  __device__ __forceinline__ int sub_unmasked(int nlo) const { return nlo + j; }
 };
 
 // OFF32: every Q / dO row a workgroup reads lies below 2 GiB of its base
@@ -184,10 +193,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const i32x4_t q_rs = raw_rsrc(q_head0), do_rs = raw_rsrc(do_head0);
   const int q_hs2 = static_cast<int>(p.q.sh * 2), q_ss2 = static_cast<int>(p.q.ss * 2);
   const int do_hs2 = static_cast<int>(p.dout.sh * 2), do_ss2 = static_cast<int>(p.dout.ss * 2);
-  auto issue = [&](int st, const StepWalk& w) {
+  auto issue = [&](int st, const StepWalk& w, auto unmasked_tag) {
     if (st >= nsteps) return;
     const int g = w.g;
-    const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
+    const int q0 = qstart + (decltype(unmasked_tag)::value ? w.sub_unmasked(nlo) : w.sub(nlo, nsub)) * BMQ;
     const uint32_t buf = bufof(st);
     const char* qg = q_head0 + g * p.q.sh * 2;
     const char* dog = do_head0 + g * p.dout.sh * 2;
@@ -208,9 +217,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
     }
   };
-  issue(0, wi);
+  issue(0, wi, std::false_type{});
   wi.next(per_m, per_u, G);
-  issue(1, wi);
+  issue(1, wi, std::false_type{});
   wi.next(per_m, per_u, G);
 
   v8 kf[ND16], vf[ND16];
@@ -325,8 +334,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const i32x4_t ds_rs = raw_rsrc(ds_head0);
   const uint32_t ds_voff = (ds_lane + (16 * hh) * 8) * 2;
   const int ds_tph1k = static_cast<int>(ds_tph * 1024);
-  auto ds_store = [&](const StepWalk& w) {
-    const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
+  auto ds_store = [&](const StepWalk& w, auto unmasked_tag) {
+    const int q0 = qstart + (decltype(unmasked_tag)::value ? w.sub_unmasked(nlo) : w.sub(nlo, nsub)) * BMQ;
     const u32x4 s0 = __builtin_bit_cast(u32x4, sa2[0]), s1 = __builtin_bit_cast(u32x4, sa2[1]);
     if constexpr (OFF32) {
       const int qi = q0 >> 5;
@@ -347,7 +356,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   auto slot_generic = [&](int j) {
     wait_vm<0>();  // sub-tile j + 1
     __builtin_amdgcn_s_barrier();
-    issue(j + 2, wi);
+    issue(j + 2, wi, std::false_type{});
     wi.next(per_m, per_u, G);
     if (j >= 1 && !skipped(j - 1)) dvdk(j - 1, pa, sa);
     if (j + 1 < nsteps && !skipped(j + 1)) sdp(j + 1, sn, dn2);
@@ -356,7 +365,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         elementwise(j, std::true_type{});
       else
         elementwise(j, std::false_type{});
-      if constexpr (DS) ds_store(wc);
+      if constexpr (DS) ds_store(wc, std::false_type{});
     }
     wc.next(per_m, per_u, G);
     rotate();
@@ -372,8 +381,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     // stores, which may stay in flight.
     wait_vm<DS ? 4 : 0>();
     __builtin_amdgcn_s_barrier();
-    issue(j + 2, wi);
-    wi.next(per_m, per_u, G);
+    issue(j + 2, wi, std::true_type{});
+    wi.next_unmasked(per_u);
     const TrBase<D> tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
     const RowBase<D> rq = at_tile(rb, bufof(j + 1)), rd = at_tile(rb, bufof(j + 1) + TILE);
     const uint32_t ml = bufof(j) + 2 * TILE;
@@ -481,8 +490,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       (tick(std::integral_constant<int, t>{}), ...);
     }(std::make_integer_sequence<int, 32>{});
     kahan(tdn, tdb);
-    if constexpr (DS) ds_store(wc);
-    wc.next(per_m, per_u, G);
+    if constexpr (DS) ds_store(wc, std::true_type{});
+    wc.next_unmasked(per_u);
     rotate();
   };
 
