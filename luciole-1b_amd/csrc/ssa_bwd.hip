@@ -717,11 +717,12 @@ __global__ __launch_bounds__(256) void ssa_reduce_partials_kernel(const float* p
 
 // ---------------------------------------------------------------------------
 // dQ from the dS' workspace written by the dK/dV kernel: dQ = scale n b dS' K,
-// no recompute.  128 queries per workgroup (4 waves x 32), keys in tiles of 64.
-// Two LDS rings, both filled by direct-to-LDS loads: K tiles (L2-resident)
+// no recompute.  32 NW queries per workgroup (NW waves x 32), keys in tiles of
+// 64.  Two LDS rings, both filled by direct-to-LDS loads: K tiles (L2-resident)
 // NK buffers loaded PFK steps ahead; the four 1 KB dS' tiles of every wave
-// (streamed from HBM) NDS buffers loaded PFD > PFK steps ahead; 80 KB in all
-// at D = 128, so two workgroups share a CU.  Step t issues K(t + PFK), then
+// (streamed from HBM) NDS buffers loaded PFD > PFK steps ahead.  At D = 128,
+// NW = 8: 128 KB, one workgroup per CU, each K tile read once per 256 queries
+// (4 % faster than two 4-wave workgroups per CU, which read K twice as often).  Step t issues K(t + PFK), then
 // dS'(t + PFD), so dS'(t) is older than K(t) and one counted wait covers both:
 // the loads issued after K(t) -- the 4 dS' loads of its own step and the
 // KP + 4 of each of the PFK - 1 steps after it -- may be outstanding.  Every step issues the same
@@ -730,16 +731,16 @@ __global__ __launch_bounds__(256) void ssa_reduce_partials_kernel(const float* p
 // dQ^T += K^T dS'^T on 32x32x16 MFMAs: A = K^T by transpose reads (rows d,
 // contraction over keys in the order 8 hi + 4 hh + e), B = the stored tile,
 // transposed on the way out of LDS into that same key order.
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
+template <typename T, int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
   using BL = BlockLayout<D>;
-  constexpr int BM = 128, BN = 64, ND32 = D / 32;
+  constexpr int BM = 32 * NW, BN = 64, ND32 = D / 32;
   constexpr int NK = 2, PFK = 1, NDS = 3, PFD = 2;
   constexpr int KTILE = BN * D * 2;
-  constexpr int DSTAGE = 4 * 4096;             // 4 waves x 4 dS' tiles
-  constexpr int KP = (BN / 32) * BL::IPB / 4;  // K load pieces per wave and tile
+  constexpr int DSTAGE = NW * 4096;             // NW waves x 4 dS' tiles
+  constexpr int KP = (BN / 32) * BL::IPB / NW;  // K load pieces per wave and tile
   static_assert(KP >= 1, "K tile split");
   static_assert(PFD > PFK && PFK >= 1 && PFK < NK && PFD < NDS, "ring depths");
   __shared__ __attribute__((aligned(1024))) char smem[NK * KTILE + NDS * DSTAGE];
@@ -796,9 +797,9 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_ds_kernel(BwdParams p) {
 
   auto issue_k = [&](int t) {
     if constexpr (ROWSWZ)
-      rowswz_load<BN, 4>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, rlk);
+      rowswz_load<BN, NW>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, rlk);
     else
-      tile_load_async<D, BN, 4>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, llk);
+      tile_load_async<D, BN, NW>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, llk);
   };
   auto issue_ds = [&](int t) {
     const uint32_t dst = lds_ds + (t % NDS) * DSTAGE + wave * 4096;
@@ -918,13 +919,23 @@ static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// dS' K pass: 8 waves (256 queries, one 128 KB workgroup per CU) at head
+// dim 128, so each K tile is read once per 256 queries; 4 waves otherwise.
+template <int D>
+constexpr int dq_ds_waves() {
+  return D == 128 ? 8 : 4;
+}
+
 template <typename T, int D, bool CAUSAL>
 static hipError_t dq_t(const BwdParams& p, hipStream_t s) {
-  const int grid = ((p.N + 127) / 128) * p.B * p.Hq;
-  if (p.ds != nullptr)
-    hipLaunchKernelGGL((ssa_bwd_dq_ds_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, s, p);
-  else
+  if (p.ds != nullptr) {
+    constexpr int NW = dq_ds_waves<D>();
+    const int grid = ((p.N + 32 * NW - 1) / (32 * NW)) * p.B * p.Hq;
+    hipLaunchKernelGGL((ssa_bwd_dq_ds_kernel<T, D, CAUSAL, NW>), dim3(grid), dim3(NW * 64), 0, s, p);
+  } else {
+    const int grid = ((p.N + 127) / 128) * p.B * p.Hq;
     hipLaunchKernelGGL((ssa_bwd_dq_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 
