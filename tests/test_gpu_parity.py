@@ -126,3 +126,38 @@ def test_determinism_bitwise(gpu):
             runs.append((out, m) + tuple(grads))
         for a, c in zip(runs[0], runs[1]):
             assert torch.equal(a, c), f"non-deterministic result ({layout})"
+
+
+@pytest.mark.parametrize("ds", [True, False], ids=["ds", "recompute"])
+def test_dkdv_wide_row_range_bitwise(gpu, ds):
+    """dK/dV addresses a workgroup's Q / dO rows with 32-bit offsets when they
+    lie within 2 GiB of the workgroup's first q-head, and with 64-bit
+    arithmetic otherwise.  A q view whose two heads (one kv-head, G = 2) lie
+    2 GiB apart takes the second path; its gradients must equal, bit for bit,
+    those of the same values in a contiguous q (the first path): only the
+    addressing differs."""
+    from SSA.ssa_triton_kernel import ssa_flash_attn_backward, ssa_flash_attn_forward
+
+    print(f"[gpu case] dK/dV 64-bit row range ds={int(ds)}", file=sys.stderr, flush=True)
+    N, D, step = 256, 128, 1 << 15  # head stride 2**30 elements = 2 GiB of bf16
+    g = torch.Generator().manual_seed(5)
+    vals = (torch.randn(1, 2, N, D, generator=g) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(1, 1, N, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    v = (torch.randn(1, 1, N, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    do = torch.randn(1, 2, N, D, generator=g).to(torch.bfloat16).to(gpu)
+    big = torch.empty(1, step + 1, N, D, device=gpu, dtype=torch.bfloat16)  # 2.1 GB
+    q_wide = big[:, ::step]
+    q_wide.copy_(vals.to(gpu))
+    assert q_wide.stride(1) == 1 << 30
+    q = q_wide.contiguous()
+    n = torch.tensor(1.5, device=gpu)
+    b = torch.tensor(0.8, device=gpu)
+    s = 1.0 / math.sqrt(D)
+    out, m = ssa_flash_attn_forward(q, k, v, s, n, b, causal=True)
+    wide = ssa_flash_attn_backward(q_wide, k, v, out, do, m, s, n, b, causal=True, ds=ds)
+    dense = ssa_flash_attn_backward(q, k, v, out, do, m, s, n, b, causal=True, ds=ds)
+    torch.cuda.synchronize()
+    for a, c in zip(wide, dense):
+        assert torch.equal(a, c)
+    del big, q_wide
+    torch.cuda.empty_cache()
