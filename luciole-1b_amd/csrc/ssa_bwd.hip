@@ -4,9 +4,10 @@
 // Replaces _ssa_attn_bwd_preprocess, _ssa_attn_bwd_dkdv, _ssa_attn_bwd_dq and
 // _ssa_attn_bwd (training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:
 // 267-298, 305-401, 408-481, 488-719) and the dn_partial/db_partial sums
-// (:894-895).  As in the reference, dQ is produced by its own pass with the
-// scores recomputed, so no floating-point atomics are needed anywhere and the
-// results are bitwise reproducible.
+// (:894-895).  As in the reference, dQ is produced by its own pass, so no
+// floating-point atomics are needed anywhere and the results are bitwise
+// reproducible: either recomputing the scores (the reference's way) or, with
+// a dS' workspace written by dK/dV, as a streaming product dS' K.
 //
 // Per valid (query i, key j), with s = scale * q_i.k_j, u = b|s|,
 // sL = sign(s) log2(1+u) and M_i the base-2 normaliser saved by the forward:
