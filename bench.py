@@ -168,7 +168,7 @@ def main():
                          "of sustained load; train1b 2)")
     ap.add_argument("--config", default="s4096",
                     choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS) + sorted(DECODE_CONFIGS) + sorted(TRAIN_CONFIGS))
-    ap.add_argument("--kernel-iters", type=int, default=20, help="launches per kernel for per-kernel timing")
+    ap.add_argument("--kernel-iters", type=int, default=50, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     ap.add_argument("--pmc-pass", action="store_true",
@@ -258,15 +258,16 @@ def main():
             e.record(stream)
         torch.cuda.synchronize()
         ts = sorted(a.elapsed_time(e) for a, e in evs)
-        return sum(ts) / len(ts), ts[len(ts) // 2]
+        pct = lambda f: ts[min(len(ts) - 1, int(f * len(ts)))]
+        return sum(ts) / len(ts), {"median_ms": ts[len(ts) // 2], "p10_ms": pct(0.1), "p90_ms": pct(0.9)}
 
     it = args.kernel_iters
     kernels = {}
-    avg, med = time_launch(lambda: ssa_flash_attn_forward(q, k, v, scale, n, bb, causal), it)
-    kernels["ssa_fwd_kernel"] = {"avg_ms": avg, "median_ms": med, "alg_flop": flops_fwd}
+    avg, spread = time_launch(lambda: ssa_flash_attn_forward(q, k, v, scale, n, bb, causal), it)
+    kernels["ssa_fwd_kernel"] = {"avg_ms": avg, **spread, "alg_flop": flops_fwd}
     for stage in BackwardLaunch.STAGES:
-        avg, med = time_launch(lambda s=stage: launch.run_stage(s), it)
-        kernels[f"ssa_bwd_{stage}_kernel"] = {"avg_ms": avg, "median_ms": med}
+        avg, spread = time_launch(lambda s=stage: launch.run_stage(s), it)
+        kernels[f"ssa_bwd_{stage}_kernel"] = {"avg_ms": avg, **spread}
     # Algorithmic work per launch: dK/dV does QK^T, dP, dV, dK (8 D per pair);
     # dQ adds only its dQ product (2 D per pair); preprocess moves O, dO, Delta.
     # On the dS' workspace path dQ streams the workspace (read once) plus K and
@@ -328,12 +329,34 @@ def main():
         "roofline": roofline,
         "cpu_baseline": None,
         "device": torch.cuda.get_device_name(0),
-        "cu_count": torch.cuda.get_device_properties(0).multi_processor_count,
+        **device_clock_and_peak(),
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(S, D, causal)
     print(json.dumps(result))
+
+
+def device_clock_and_peak():
+    """CU count and peak engine clock of device 0 (hipDeviceGetAttribute,
+    hipDeviceAttributeClockRate = 5 in hip_runtime_api.h, kHz), and the dense
+    bf16 MFMA peak they imply (4096 FLOP per clock per CU); the figures above
+    use the published 2516.6 TFLOP/s."""
+    import ctypes
+
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    info = {"cu_count": cus, "max_engine_clock_mhz": None, "bf16_peak_at_clock_tflops": None}
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+        khz = ctypes.c_int(0)
+        if hip.hipDeviceGetAttribute(ctypes.byref(khz), 5, torch.cuda.current_device()) == 0 and khz.value > 0:
+            info["max_engine_clock_mhz"] = khz.value / 1e3
+            info["bf16_peak_at_clock_tflops"] = cus * khz.value * 1e3 * 4096 / 1e12
+    except OSError:
+        pass
+    return info
 
 
 def bench_varlen(args, dev):
