@@ -506,22 +506,44 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   for (; j + 1 < nsteps; ++j) slot_fast(j);
   for (; j <= nsteps; ++j) slot_generic(j);
 
-  // Store dK (scaled by scale * n * b) and dV: lane holds d = 32*db + l32,
-  // key rows crow(r, hh) of this wave's 32 keys.
-  const float kscale = p.scale * n * *p.b_ptr;
-  T* dkg = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;
-  T* dvg = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh;
+  // Store dK (scaled by scale * n * b) and dV.  The lane holds d = 32 db + l32
+  // of key rows crow(r, hh); each wave turns its 32 keys x D through its own
+  // LDS tile, [d][key] with 72-byte rows, so that every lane stores 8 bytes
+  // (4 consecutive d of one key) per instruction.  Write: lane (l32, hh), keys
+  // 8 a + 4 hh .. + 3 of row d.  Transposed read t: in 16-lane group g, lane
+  // 4 e + q supplies row 8 t + 4 (g >> 1) + e, keys 16 (g & 1) + 4 q .. + 3, so
+  // lane 16 g + i receives key 16 (g & 1) + i, d = 8 t + 4 (g >> 1) + (0..3).
+  __syncthreads();  // every wave is done with the sub-tile ring (no loads in flight)
+  constexpr int RS = 72;
+  const uint32_t tile = lds0 + wave * (D * RS);
+  const uint32_t wr0 = tile + l32 * RS + hh * 8;
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const uint32_t rd0 = tile + (4 * (g16 >> 1) + (s16 >> 2)) * RS + (16 * (g16 & 1) + 4 * (s16 & 3)) * 2;
+  const int okey = k0w + 16 * (g16 & 1) + s16;
+  const int od0 = 4 * (g16 >> 1);
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  auto put = [&](const f32x16* acc, float scale, const Tensor4& t) {
 #pragma unroll
-  for (int db = 0; db < ND32; ++db) {
+    for (int db = 0; db < ND32; ++db) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kr = k0w + crow(r, hh);
-      if (kr < N) {
-        dkg[kr * p.dk.ss + db * 32 + l32] = static_cast<T>(dk[db][r] * kscale);
-        dvg[kr * p.dv.ss + db * 32 + l32] = static_cast<T>(dv[db][r]);
+      for (int a = 0; a < 4; ++a) {
+        v4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[db][4 * a + e] * scale);
+        *(__attribute__((address_space(3))) v4*)(uintptr_t)(wr0 + db * 32 * RS + a * 16) = w;
       }
     }
-  }
+    T* row = static_cast<T*>(const_cast<void*>(t.ptr)) + sv.off(t, b) + hk * t.sh + min(okey, N - 1) * t.ss + od0;
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+      const v4 r = __builtin_bit_cast(
+          v4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                  (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(rd0 + i * 8 * RS)));
+      if (okey < N) *reinterpret_cast<v4*>(row + 8 * i) = r;
+    }
+  };
+  put(dk, p.scale * n * *p.b_ptr, p.dk);
+  put(dv, 1.f, p.dv);
 
   // dn / db partial of this workgroup: lane butterfly, then waves in order.
   float pdn = dn_acc - dn_c, pdb = db_acc - db_c;
