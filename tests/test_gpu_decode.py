@@ -87,6 +87,17 @@ def test_decode_matches_oracle(gpu, D, B, Hq, Hkv, cap, lens, splits):
     _check(gpu, q, kc, vc, lens, num_splits=splits, label=label)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,cap,D", [(16, 16, 16, 4096, 128), (16, 32, 8, 4096, 64)],
+                         ids=["decode_s4096", "decode_gqa_d64"])
+def test_decode_full_size(gpu, B, Hq, Hkv, cap, D):
+    """The benchmark's decode steps at full size (every cache full at 4096
+    keys, the default splits) against the oracle on every head."""
+    label = f"decode full size B={B} Hq={Hq} Hkv={Hkv} cap={cap} D={D}"
+    print(f"[gpu case] {label}", file=sys.stderr, flush=True)
+    q, kc, vc = _case(gpu, B, Hq, Hkv, cap, D, torch.bfloat16)
+    _check(gpu, q, kc, vc, [cap] * B, label=label)
+
+
 @pytest.mark.parametrize("n_val", [0.0, -3.484375, -302.0, 5.0])
 def test_decode_scalars(gpu, n_val):
     label = f"decode n={n_val}"
