@@ -237,7 +237,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     dv[i] = f32x16{};
   }
   float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;
-  f32x16 sc, dc, sn, dn2;  // S, dP of sub-tiles j and j + 1
+  // S, dP of sub-tiles j and j + 1.  Zero-initialised: a skipped step leaves
+  // them as they were, and the masked fast slot multiplies their entries by a
+  // zero P, which must stay zero (finite operands).
+  f32x16 sc = f32x16{}, dc = f32x16{}, sn = f32x16{}, dn2 = f32x16{};
   v8 pa[2], sa[2], pa2[2], sa2[2];  // P^T, dS'^T operands of sub-tiles j - 1 and j
 
   auto kahan = [&](float tdn, float tdb) {
@@ -367,23 +370,47 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       else
         elementwise(j, std::false_type{});
       if constexpr (DS) ds_store(wc, std::false_type{});
+    } else {
+      // the masked fast slot after this one runs dV/dK of step j
+      // unconditionally: zero operands add nothing
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) pa2[ks] = sa2[ks] = zero8<v8>();
     }
     wc.next(per_m, per_u, G);
     rotate();
   };
 
   // ---- steady-state slot: sub-tiles j - 1, j, j + 1 unmasked ----
-  auto slot_fast = [&](int j) {
+  // MASKED: the same slot over masked steps (the causal diagonal, a partial
+  // last sub-tile, a key block at the sequence end): P is zeroed outside the
+  // mask, every MFMA runs (a skipped step contributes zeros), and only a step
+  // with a valid pair stores its dS' tile.
+  auto slot_fast = [&](int j, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr int NG = 4 * ND32 + 2 * ND16;  // MFMAs per slot
     constexpr int STRIDE = 32 / NG;           // ticks per MFMA
     // Sub-tile j + 1 (issued in slot j - 1).  The vector-memory counter also
-    // counts stores, in issue order: slot j - 1 (always a storing slot here,
-    // the fast one or the first unmasked generic one) ended with its four dS'
-    // stores, which may stay in flight.
-    wait_vm<DS ? 4 : 0>();
+    // counts stores, in issue order: slot j - 1 ended with its four dS' stores
+    // (an unmasked slot always stores; a masked one unless its step was
+    // skipped), which may stay in flight.
+    if constexpr (!DS) {
+      wait_vm<0>();
+    } else if constexpr (MASKED) {
+      if (skipped(j - 1))
+        wait_vm<0>();
+      else
+        wait_vm<4>();
+    } else {
+      wait_vm<4>();
+    }
     __builtin_amdgcn_s_barrier();
-    issue(j + 2, wi, std::true_type{});
-    wi.next_unmasked(per_u);
+    issue(j + 2, wi, std::integral_constant<bool, !MASKED>{});
+    if constexpr (MASKED)
+      wi.next(per_m, per_u, G);
+    else
+      wi.next_unmasked(per_u);
+    // masked: query row of element e is qm + 8 (e >> 2) + (e & 3)
+    const int qm = qstart + wc.sub(nlo, nsub) * BMQ + 4 * hh;
     const TrBase<D> tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
     const RowBase<D> rq = at_tile(rb, bufof(j + 1)), rd = at_tile(rb, bufof(j + 1) + TILE);
     const uint32_t ml = bufof(j) + 2 * TILE;
@@ -444,6 +471,11 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       const float x = sc[e];
       slv[e] = copysignf(Lv[e], x);
       pv[e] = fast_exp2(fmaf(n, slv[e], -mq[e >> 2][e & 3]));
+      if constexpr (MASKED) {
+        const int qi = qm + 8 * (e >> 2) + (e & 3);
+        const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
+        pv[e] = valid ? pv[e] : 0.f;
+      }
       ddv[e] = dc[e] - dq4[e >> 2][e & 3];
       pin(pv[e]);
       pin(ddv[e]);
@@ -491,8 +523,13 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       (tick(std::integral_constant<int, t>{}), ...);
     }(std::make_integer_sequence<int, 32>{});
     kahan(tdn, tdb);
-    if constexpr (DS) ds_store(wc, std::true_type{});
-    wc.next_unmasked(per_u);
+    if constexpr (DS) {
+      if (!MASKED || !skipped(j)) ds_store(wc, std::integral_constant<bool, !MASKED>{});
+    }
+    if constexpr (MASKED)
+      wc.next(per_m, per_u, G);
+    else
+      wc.next_unmasked(per_u);
     rotate();
   };
 
@@ -501,9 +538,15 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   __builtin_amdgcn_s_barrier();
   if (!skipped(0)) sdp(0, sn, dn2);
   rotate();
-  int j = 0;
+  // generic slot 0 (no dV/dK yet), masked fast slots while steps j - 1 .. j + 1
+  // exist and j is masked, generic up to the first unmasked step (so every
+  // unmasked fast slot follows a storing slot), unmasked fast slots, generic
+  // drain
+  slot_generic(0);
+  int j = 1;
+  for (; j < nmasked && j + 1 < nsteps; ++j) slot_fast(j, std::true_type{});
   for (; j <= nmasked && j <= nsteps; ++j) slot_generic(j);
-  for (; j + 1 < nsteps; ++j) slot_fast(j);
+  for (; j + 1 < nsteps; ++j) slot_fast(j, std::false_type{});
   for (; j <= nsteps; ++j) slot_generic(j);
 
   // Store dK (scaled by scale * n * b) and dV.  The lane holds d = 32 db + l32
