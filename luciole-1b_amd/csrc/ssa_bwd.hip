@@ -539,12 +539,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   if (!skipped(0)) sdp(0, sn, dn2);
   rotate();
   // generic slot 0 (no dV/dK yet), masked fast slots while steps j - 1 .. j + 1
-  // exist and j is masked, generic up to the first unmasked step (so every
-  // unmasked fast slot follows a storing slot), unmasked fast slots, generic
-  // drain
+  // exist up to the first unmasked step (which passes every mask and always
+  // stores, so every unmasked fast slot follows a storing slot), generic if
+  // that step ends the sequence, unmasked fast slots, generic drain
   slot_generic(0);
   int j = 1;
-  for (; j < nmasked && j + 1 < nsteps; ++j) slot_fast(j, std::true_type{});
+  for (; j <= nmasked && j + 1 < nsteps; ++j) slot_fast(j, std::true_type{});
   for (; j <= nmasked && j <= nsteps; ++j) slot_generic(j);
   for (; j + 1 < nsteps; ++j) slot_fast(j, std::false_type{});
   for (; j <= nsteps; ++j) slot_generic(j);
