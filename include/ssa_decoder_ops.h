@@ -1,0 +1,58 @@
+/*
+ * Fused element-wise operators of the SSA decoder layer (gfx950), next to the
+ * attention path: the callers either side of it in a transformer layer.
+ *
+ * Same rules as ssa_mi355x.h: the caller owns every buffer, the call only
+ * enqueues on `stream` (a hipStream_t, NULL = default stream) and returns a
+ * status before any launch when an argument is invalid.
+ */
+#ifndef SSA_DECODER_OPS_H
+#define SSA_DECODER_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  SSA_OPS_OK = 0,
+  SSA_OPS_ERR_NULL_POINTER = 1,
+  SSA_OPS_ERR_SHAPE = 2,
+  SSA_OPS_ERR_DTYPE = 3,
+  SSA_OPS_ERR_ALIGNMENT = 4,
+  SSA_OPS_ERR_LAUNCH = 5
+};
+
+/*
+ * Rotary position embedding, rotate-half form, applied to q or k before the
+ * core attention.  Replaces the rotary step of the Megatron SelfAttention that
+ * the reference's SSA layer spec builds
+ * (training/train/train_ssa_triton/SSA/ssa_triton_layer_specs.py:96-127;
+ * Megatron's default non-interleaved RoPE, rotary base 10000).
+ *
+ * x: [seqlen, batch, heads, head_dim] in bf16/fp16 with element strides
+ * x_stride_{s,b,h} (stride 1 over head_dim); y: contiguous, same shape.
+ * cos, sin: fp32 [seqlen, head_dim / 2], row s = cos / sin of s * inv_freq.
+ * inverse = 1 rotates by the negative angle (the backward).  head_dim 64 or
+ * 128; x, y 8-byte aligned, strides multiples of 4 elements, tables 16-byte
+ * aligned.
+ */
+typedef struct {
+  const void* x;
+  int64_t x_stride_s, x_stride_b, x_stride_h;
+  void* y;
+  const float* cos;
+  const float* sin;
+  int32_t seqlen, batch, heads, head_dim;
+  int32_t dtype; /* 0 = bf16, 1 = fp16 */
+  int32_t inverse;
+} ssa_rope_args;
+
+int32_t ssa_rope(const ssa_rope_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSA_DECODER_OPS_H */

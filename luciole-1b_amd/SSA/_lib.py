@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "ssa_decode_num_splits",
     "ssa_decode_workspace_bytes",
     "ssa_decode",
+    "ssa_rope",  # include/ssa_decoder_ops.h
 )
 
 ABI_VERSION = 4
@@ -107,6 +108,26 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    """ssa_rope_args of include/ssa_decoder_ops.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_stride_s", ctypes.c_int64),
+        ("x_stride_b", ctypes.c_int64),
+        ("x_stride_h", ctypes.c_int64),
+        ("y", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("seqlen", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("inverse", ctypes.c_int32),
+    ]
+
+
 class VarlenFwdArgs(ctypes.Structure):
     _fields_ = [("dense", FwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
 
@@ -158,7 +179,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
     for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs),
-                       ("ssa_decode", DecodeArgs)):
+                       ("ssa_decode", DecodeArgs), ("ssa_rope", RopeArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]

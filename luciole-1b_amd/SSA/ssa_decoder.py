@@ -22,6 +22,7 @@ re-runs the whole prefix per token, training/train/train_ssa_triton/generate_tri
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import List, Optional
@@ -50,6 +51,7 @@ class SSADecoderConfig:
     learnable_ssa: bool = True
     learnable_b: bool = False
     init_std: float = 0.02
+    fused_rope: bool = True  # ssa_rope on the GPU (False: the PyTorch form)
 
     def num_parameters(self) -> int:
         h, f, v = self.hidden_size, self.ffn_hidden_size, self.vocab_size
@@ -81,10 +83,51 @@ def rope_tables(positions: torch.Tensor, dim: int, base: float):
 
 
 def apply_rope(x, cos, sin):
+    """Rotate-half RoPE in PyTorch (fp32 math): the reference form the fused
+    kernel is tested against."""
     xf = x.float()
     x1, x2 = xf.chunk(2, dim=-1)
     rot = torch.cat([-x2, x1], dim=-1)
     return (xf * cos + rot * sin).to(x.dtype)
+
+
+def _rope_launch(x, cos_h, sin_h, inverse: bool):
+    from . import _lib
+
+    if x.dim() != 4 or x.stride(-1) != 1:
+        x = x.contiguous()
+    S, B, H, D = x.shape
+    y = torch.empty((S, B, H, D), device=x.device, dtype=x.dtype)
+    args = _lib.RopeArgs(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2), y.data_ptr(), cos_h.data_ptr(),
+                         sin_h.data_ptr(), S, B, H, D, 0 if x.dtype == torch.bfloat16 else 1, int(inverse))
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check(_lib.lib().ssa_rope(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_rope")
+    return y
+
+
+class FusedRoPE(torch.autograd.Function):
+    """apply_rope as one HIP pass each way (``ssa_rope``; the backward rotates
+    by the negative angle).  x: [S, B, H, D] bf16/fp16, D in {64, 128}."""
+
+    @staticmethod
+    def forward(ctx, x, cos_h, sin_h):
+        ctx.save_for_backward(cos_h, sin_h)
+        return _rope_launch(x, cos_h, sin_h, False)
+
+    @staticmethod
+    def backward(ctx, dy):
+        cos_h, sin_h = ctx.saved_tensors
+        return _rope_launch(dy, cos_h, sin_h, True), None, None
+
+
+def rope(x, cos, sin, cos_h=None, sin_h=None):
+    """RoPE for the layer: the fused kernel for bf16/fp16 inputs with head dim
+    64 or 128 on the GPU (``cos_h`` / ``sin_h`` its tables), PyTorch otherwise."""
+    if (cos_h is not None and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+            and x.shape[-1] in (64, 128)):
+        return FusedRoPE.apply(x, cos_h, sin_h)
+    return apply_rope(x, cos, sin)
 
 
 class SelfAttention(nn.Module):
@@ -98,16 +141,17 @@ class SelfAttention(nn.Module):
                                            learnable_b=cfg.learnable_b)
         self.linear_proj = nn.Linear(self.np * self.hn, cfg.hidden_size, bias=False)
 
-    def _qkv(self, x, cos, sin):
+    def _qkv(self, x, rot):
         S, B = x.shape[0], x.shape[1]
         g = self.np // self.ng
         mixed = self.linear_qkv(x).view(S, B, self.ng, (g + 2) * self.hn)
         q, k, v = torch.split(mixed, [g * self.hn, self.hn, self.hn], dim=-1)
         q = q.reshape(S, B, self.np, self.hn)
-        return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v
+        return rope(q, *rot), rope(k, *rot), v
 
-    def forward(self, x, cos, sin, cache: Optional[SSAKVCache] = None):
-        q, k, v = self._qkv(x, cos, sin)
+    def forward(self, x, rot, cache: Optional[SSAKVCache] = None):
+        """rot = (cos, sin, cos_h, sin_h) from ``SSADecoder.rotary``."""
+        q, k, v = self._qkv(x, rot)
         if cache is None:
             ctx = self.core_attention(q, k, v)
         elif x.shape[0] == 1:
@@ -137,8 +181,8 @@ class TransformerLayer(nn.Module):
         self.pre_mlp_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
         self.mlp = MLP(cfg)
 
-    def forward(self, x, cos, sin, cache=None):
-        x = x + self.self_attention(self.input_layernorm(x), cos, sin, cache)
+    def forward(self, x, rot, cache=None):
+        x = x + self.self_attention(self.input_layernorm(x), rot, cache)
         return x + self.mlp(self.pre_mlp_layernorm(x))
 
 
@@ -168,10 +212,19 @@ class SSADecoder(nn.Module):
         S = input_ids.shape[1]
         x = self.embedding(input_ids.t())  # [S, B, h]
         pos = torch.arange(start_pos, start_pos + S, device=input_ids.device)
-        cos, sin = rope_tables(pos, self.cfg.kv_channels, self.cfg.rotary_base)
+        rot = self.rotary(pos)
         for i, layer in enumerate(self.layers):
-            x = layer(x, cos, sin, None if caches is None else caches[i])
+            x = layer(x, rot, None if caches is None else caches[i])
         return self.output_layer(self.final_layernorm(x))
+
+    def rotary(self, positions):
+        """(cos, sin) [S, 1, 1, D] for the PyTorch form and, with
+        ``fused_rope``, the fp32 [S, D / 2] tables of the fused kernel."""
+        cos, sin = rope_tables(positions, self.cfg.kv_channels, self.cfg.rotary_base)
+        if not self.cfg.fused_rope:
+            return cos, sin, None, None
+        half = self.cfg.kv_channels // 2
+        return cos, sin, cos[:, 0, 0, :half].contiguous(), sin[:, 0, 0, :half].contiguous()
 
     def loss(self, input_ids, labels):
         logits = self(input_ids)  # [S, B, V]

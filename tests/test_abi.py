@@ -279,3 +279,28 @@ def test_decode_validation(field, value, status):
 
 def test_decode_null_args():
     assert _lib.lib().ssa_decode(None, None) == _lib.SSA_ERR_NULL_POINTER
+
+
+def _rope_args(**kw):
+    a = _lib.RopeArgs(FAKE, 16 * 128, 128, 128 * 0 + 128, FAKE, FAKE, FAKE, 4, 1, 16, 128, 0, 0)
+    a.x_stride_h = 128
+    a.x_stride_b = 16 * 128
+    a.x_stride_s = 16 * 128
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "field,value,status",
+    [
+        ("x", None, 1), ("y", None, 1), ("cos", None, 1), ("sin", None, 1),
+        ("seqlen", 0, 2), ("heads", -1, 2), ("head_dim", 96, 2), ("head_dim", 32, 2),
+        ("dtype", 2, 3),
+        ("x", FAKE + 4, 4), ("cos", FAKE + 8, 4), ("x_stride_h", 130, 4), ("x_stride_s", -128, 4),
+    ],
+)
+def test_rope_validation(field, value, status):
+    """ssa_rope (include/ssa_decoder_ops.h) rejects bad arguments on the host."""
+    a = _rope_args(**{field: value})
+    assert _lib.lib().ssa_rope(ctypes.byref(a), None) == status

@@ -114,3 +114,70 @@ def test_decoder_cached_generation_equals_prefix_recompute(gpu):
             full = model(tokens[:, : 37 + t])[-1].float()  # the whole prefix, as the reference re-runs it
             assert _rel(step_logits[t], full) <= 2e-2, (t, _rel(step_logits[t], full))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.bfloat16), (128, torch.float16)])
+def test_fused_rope_matches_torch(gpu, D, dtype):
+    """ssa_rope (FusedRoPE) against the PyTorch rotate-half form in fp32, on a
+    strided view like the k slice of the fused QKV output, forward and
+    backward: within one unit in the last place of the dtype."""
+    from SSA.ssa_decoder import FusedRoPE, apply_rope, rope_tables
+
+    print(f"[gpu case] fused RoPE D={D} {dtype}", file=sys.stderr, flush=True)
+    torch.manual_seed(3)
+    S, B, H = 300, 2, 3
+    base = torch.randn(S, B, H, 3 * D, device=gpu).to(dtype)
+    x = base[..., D:2 * D]  # strided [S, B, H, D] view
+    cos, sin = rope_tables(torch.arange(7, 7 + S, device=gpu), D, 10000.0)
+    cos_h, sin_h = cos[:, 0, 0, :D // 2].contiguous(), sin[:, 0, 0, :D // 2].contiguous()
+    xa = x.detach().clone().requires_grad_(True)
+    xb = x.detach().clone().requires_grad_(True)
+    ya = FusedRoPE.apply(xa, cos_h, sin_h)
+    yb = apply_rope(xb.float(), cos, sin)  # fp32 reference
+    w = torch.randn_like(yb)
+    (ya.float() * w).sum().backward()
+    (yb * w).sum().backward()
+    torch.cuda.synchronize()
+    # error bound per rotated pair (i, i + D/2): a rotation keeps the pair's
+    # norm, and both sides round inputs or outputs to the dtype once
+    tol = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
+
+    def pair_norm(t):
+        t1, t2 = t.chunk(2, dim=-1)
+        r = torch.sqrt(t1 * t1 + t2 * t2)
+        return torch.cat([r, r], dim=-1)
+
+    assert ((ya.float() - yb).abs() <= tol * pair_norm(yb) + 1e-6).all()
+    ga, gb = xa.grad.float(), xb.grad.float()
+    assert ((ga - gb).abs() <= 2 * tol * pair_norm(gb) + 1e-6).all()
+
+
+def test_decoder_fused_rope_equals_torch_rope(gpu):
+    """The same decoder with the fused RoPE kernel and with the PyTorch form:
+    logits and gradients agree to bf16-level relative error."""
+    import dataclasses
+
+    from SSA.ssa_decoder import SSADecoder
+
+    print("[gpu case] decoder fused vs torch RoPE", file=sys.stderr, flush=True)
+    torch.manual_seed(4)
+    cfg = _tiny(True)
+    model = SSADecoder(cfg).to(gpu)
+    ids = torch.randint(0, cfg.vocab_size, (2, 160), device=gpu)
+    labels = torch.randint(0, cfg.vocab_size, (2, 160), device=gpu)
+
+    def run(fused):
+        model.cfg = dataclasses.replace(cfg, fused_rope=fused)
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = model(ids)
+            loss = torch.nn.functional.cross_entropy(logits.float().view(-1, cfg.vocab_size), labels.t().reshape(-1))
+        loss.backward()
+        return logits.detach(), {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
+
+    la, ga = run(True)
+    lb, gb = run(False)
+    torch.cuda.synchronize()
+    assert _rel(la, lb) <= 1e-2, _rel(la, lb)
+    for name in ga:
+        assert _rel(ga[name], gb[name]) <= 3e-2, (name, _rel(ga[name], gb[name]))
