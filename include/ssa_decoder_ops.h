@@ -51,6 +51,47 @@ typedef struct {
 
 int32_t ssa_rope(const ssa_rope_args* args, void* stream);
 
+/*
+ * RMSNorm of the decoder layer's input and pre-MLP norms (and the final
+ * norm): y = x * (mean(x^2) + eps)^-1/2 * weight over rows of `hidden`
+ * values.  Replaces the TE/Megatron RMSNorm modules of the reference's SSA
+ * layer spec (training/train/train_ssa_triton/SSA/ssa_triton_layer_specs.py:
+ * 96-127; normalization "RMSNorm" in the run configuration).
+ *
+ * x, weight: fp32 (the residual stream and the parameter), x [rows, hidden]
+ * contiguous, 16-byte aligned; hidden a multiple of 4, at most 4096.  y is
+ * written in out_dtype (0 bf16, 1 fp16, 2 fp32: the dtype of the next GEMM's
+ * input), rstd [rows] fp32 is kept for the backward.  The backward reads dy
+ * in dy_dtype, writes dx fp32 [rows, hidden] and dweight fp32 [hidden]; its
+ * workspace holds ssa_rmsnorm_workspace_floats(rows, hidden) fp32 partial
+ * weight gradients, summed in a fixed order (deterministic).
+ */
+typedef struct {
+  const void* x;
+  const void* weight;
+  void* y;
+  float* rstd;
+  int32_t rows, hidden;
+  int32_t out_dtype;
+  float eps;
+} ssa_rmsnorm_fwd_args;
+
+typedef struct {
+  const void* x;
+  const void* weight;
+  const void* dy;
+  const float* rstd;
+  float* dx;
+  float* dweight;
+  float* workspace;
+  int32_t rows, hidden;
+  int32_t dy_dtype;
+} ssa_rmsnorm_bwd_args;
+
+int64_t ssa_rmsnorm_workspace_floats(int32_t rows, int32_t hidden);
+int32_t ssa_rmsnorm_fwd(const ssa_rmsnorm_fwd_args* args, void* stream);
+int32_t ssa_rmsnorm_bwd(const ssa_rmsnorm_bwd_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

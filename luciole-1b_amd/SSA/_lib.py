@@ -45,6 +45,9 @@ EXPORTED_SYMBOLS = (
     "ssa_decode_workspace_bytes",
     "ssa_decode",
     "ssa_rope",  # include/ssa_decoder_ops.h
+    "ssa_rmsnorm_workspace_floats",
+    "ssa_rmsnorm_fwd",
+    "ssa_rmsnorm_bwd",
 )
 
 ABI_VERSION = 4
@@ -128,6 +131,38 @@ class RopeArgs(ctypes.Structure):
     ]
 
 
+class RmsNormFwdArgs(ctypes.Structure):
+    """ssa_rmsnorm_fwd_args of include/ssa_decoder_ops.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("rstd", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class RmsNormBwdArgs(ctypes.Structure):
+    """ssa_rmsnorm_bwd_args of include/ssa_decoder_ops.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("rstd", ctypes.c_void_p),
+        ("dx", ctypes.c_void_p),
+        ("dweight", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("dy_dtype", ctypes.c_int32),
+    ]
+
+
 class VarlenFwdArgs(ctypes.Structure):
     _fields_ = [("dense", FwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
 
@@ -179,13 +214,16 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
     for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs),
-                       ("ssa_decode", DecodeArgs), ("ssa_rope", RopeArgs)):
+                       ("ssa_decode", DecodeArgs), ("ssa_rope", RopeArgs), ("ssa_rmsnorm_fwd", RmsNormFwdArgs),
+                       ("ssa_rmsnorm_bwd", RmsNormBwdArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
     i32 = ctypes.c_int32
     lib.ssa_decode_num_splits.restype = ctypes.c_int32
     lib.ssa_decode_num_splits.argtypes = [i32, i32, i32, i32, i32]
+    lib.ssa_rmsnorm_workspace_floats.restype = ctypes.c_int64
+    lib.ssa_rmsnorm_workspace_floats.argtypes = [i32, i32]
     lib.ssa_decode_workspace_bytes.restype = ctypes.c_int64
     lib.ssa_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
 

@@ -52,6 +52,7 @@ class SSADecoderConfig:
     learnable_b: bool = False
     init_std: float = 0.02
     fused_rope: bool = True  # ssa_rope on the GPU (False: the PyTorch form)
+    fused_norm: bool = True  # ssa_rmsnorm_* on the GPU (False: the PyTorch form)
 
     def num_parameters(self) -> int:
         h, f, v = self.hidden_size, self.ffn_hidden_size, self.vocab_size
@@ -61,13 +62,69 @@ class SSADecoderConfig:
         return self.num_layers * per_layer + 2 * v * h + h
 
 
+_OPS_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+class FusedRMSNormFn(torch.autograd.Function):
+    """RMSNorm of fp32 rows as one HIP pass each way (``ssa_rmsnorm_fwd`` /
+    ``ssa_rmsnorm_bwd``), the output written in ``out_dtype`` (the next GEMM's
+    input dtype under autocast)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, out_dtype):
+        from . import _lib
+
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        T, H = x2.shape
+        y = torch.empty((T, H), device=x.device, dtype=out_dtype)
+        rstd = torch.empty(T, device=x.device, dtype=torch.float32)
+        w = weight.contiguous()
+        args = _lib.RmsNormFwdArgs(x2.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr(), T, H,
+                                   _OPS_DTYPES[out_dtype], float(eps))
+        with torch.cuda.device(x.device):
+            stream = torch.cuda.current_stream(x.device).cuda_stream
+            _lib.check(_lib.lib().ssa_rmsnorm_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_rmsnorm_fwd")
+        ctx.save_for_backward(x2, w, rstd)
+        ctx.shape = shape
+        return y.view(shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        from . import _lib
+
+        x2, w, rstd = ctx.saved_tensors
+        T, H = x2.shape
+        dy2 = dy.reshape(T, H).contiguous()
+        dx = torch.empty_like(x2)
+        dw = torch.empty(H, device=x2.device, dtype=torch.float32)
+        lib = _lib.lib()
+        ws = torch.empty(int(lib.ssa_rmsnorm_workspace_floats(T, H)), device=x2.device, dtype=torch.float32)
+        args = _lib.RmsNormBwdArgs(x2.data_ptr(), w.data_ptr(), dy2.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+                                   dw.data_ptr(), ws.data_ptr(), T, H, _OPS_DTYPES[dy2.dtype])
+        with torch.cuda.device(x2.device):
+            stream = torch.cuda.current_stream(x2.device).cuda_stream
+            _lib.check(lib.ssa_rmsnorm_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_rmsnorm_bwd")
+        return dx.view(ctx.shape), dw.to(w.dtype), None, None
+
+
 class RMSNorm(nn.Module):
-    def __init__(self, hidden: int, eps: float):
+    def __init__(self, hidden: int, eps: float, fused: bool = True):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(hidden))
         self.eps = eps
+        self.fused = fused
 
     def forward(self, x):
+        H = x.shape[-1]
+        if (self.fused and x.is_cuda and x.dtype == torch.float32 and self.weight.dtype == torch.float32
+                and H % 4 == 0 and H <= 4096):
+            out = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
+            return FusedRMSNormFn.apply(x, self.weight, self.eps, out)
+        return self.reference(x)
+
+    def reference(self, x):
+        """The PyTorch form (fp32 math), against which the fused kernel is tested."""
         xf = x.float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         return (y * self.weight.float()).to(x.dtype)
@@ -176,9 +233,9 @@ class MLP(nn.Module):
 class TransformerLayer(nn.Module):
     def __init__(self, cfg: SSADecoderConfig, layer_number: int):
         super().__init__()
-        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps, cfg.fused_norm)
         self.self_attention = SelfAttention(cfg, layer_number)
-        self.pre_mlp_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
+        self.pre_mlp_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps, cfg.fused_norm)
         self.mlp = MLP(cfg)
 
     def forward(self, x, rot, cache=None):
@@ -192,7 +249,7 @@ class SSADecoder(nn.Module):
         self.cfg = cfg
         self.embedding = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
         self.layers = nn.ModuleList(TransformerLayer(cfg, i + 1) for i in range(cfg.num_layers))
-        self.final_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps)
+        self.final_layernorm = RMSNorm(cfg.hidden_size, cfg.norm_eps, cfg.fused_norm)
         self.output_layer = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
         self.reset_parameters()
 

@@ -1,6 +1,7 @@
 // Fused element-wise operators of the SSA decoder layer around the attention
-// path (gfx950): rotary position embedding.  One HBM pass per call in the
-// input dtype; the unfused PyTorch form makes six fp32 passes.
+// path (gfx950): rotary position embedding (one HBM pass per call in the
+// input dtype; the unfused PyTorch form makes six fp32 passes) and RMSNorm
+// (one pass forward, one backward, plus a fixed-order weight-gradient sum).
 //
 // Rotate-half RoPE (Megatron's default, non-interleaved), per (s, b, h) row of
 // D values, i < D / 2, with c = cos[s][i], t = sin[s][i]:
@@ -78,6 +79,126 @@ hipError_t launch_rope(const ssa_rope_args* a, hipStream_t st) {
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
+// ---------------------------------------------------------------------------
+// RMSNorm over rows of H fp32 values: r = (mean(x^2) + eps)^-1/2,
+// y = (x r) w in the output dtype.  Backward, with g = dy w and xh = x r:
+//   dx = r (g - xh sum(g xh) / H),  dw = sum over rows of dy xh.
+constexpr int kNormThreads = 256;
+constexpr int kNormBwdRows = 64;  // rows per backward workgroup (one dw partial each)
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();  // red is reused by consecutive calls
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <typename TO>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ w,
+                                                                   TO* __restrict__ y, float* __restrict__ rstd,
+                                                                   int H, float eps) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * H;
+  float ss = 0.f;
+  for (int c = threadIdx.x * 4; c < H; c += kNormThreads * 4) {
+    const f4 v = *reinterpret_cast<const f4*>(xr + c);
+    ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+  }
+  const float r = rsqrtf(block_sum(ss, red) / H + eps);
+  TO* yr = y + row * H;
+  for (int c = threadIdx.x * 4; c < H; c += kNormThreads * 4) {
+    const f4 v = *reinterpret_cast<const f4*>(xr + c);
+    const f4 wv = *reinterpret_cast<const f4*>(w + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yr[c + e] = static_cast<TO>(v[e] * r * wv[e]);
+  }
+  if (threadIdx.x == 0) rstd[row] = r;
+}
+
+template <typename TG>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ w,
+                                                                   const TG* __restrict__ dy,
+                                                                   const float* __restrict__ rstd,
+                                                                   float* __restrict__ dx, float* __restrict__ dw_part,
+                                                                   int T, int H) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int MAXC = 4;  // column groups of 4 per thread: H <= 4 * 4 * 256
+  __shared__ float red[4];
+  f4 acc[MAXC];
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) acc[k] = f4{0.f, 0.f, 0.f, 0.f};
+  const int r0 = blockIdx.x * kNormBwdRows;
+  const int r1 = min(T, r0 + kNormBwdRows);
+  for (int row = r0; row < r1; ++row) {
+    const float* xr = x + static_cast<int64_t>(row) * H;
+    const TG* gr = dy + static_cast<int64_t>(row) * H;
+    const float r = rstd[row];
+    f4 xh[MAXC], g[MAXC], gy[MAXC];
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const int c = (threadIdx.x + k * kNormThreads) * 4;
+      if (c < H) {
+        const f4 v = *reinterpret_cast<const f4*>(xr + c);
+        const f4 wv = *reinterpret_cast<const f4*>(w + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gy[k][e] = static_cast<float>(gr[c + e]);
+          xh[k][e] = v[e] * r;
+          g[k][e] = gy[k][e] * wv[e];
+          dot += g[k][e] * xh[k][e];
+        }
+      }
+    }
+    const float m = block_sum(dot, red) / H;
+    float* dxr = dx + static_cast<int64_t>(row) * H;
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const int c = (threadIdx.x + k * kNormThreads) * 4;
+      if (c < H) {
+        f4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = r * (g[k][e] - xh[k][e] * m);
+          acc[k][e] += gy[k][e] * xh[k][e];
+        }
+        *reinterpret_cast<f4*>(dxr + c) = o;
+      }
+    }
+  }
+  float* part = dw_part + static_cast<int64_t>(blockIdx.x) * H;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = (threadIdx.x + k * kNormThreads) * 4;
+    if (c < H) *reinterpret_cast<f4*>(part + c) = acc[k];
+  }
+}
+
+// dw[c] = sum over partials b (in order) of dw_part[b][c]
+__global__ __launch_bounds__(256) void rmsnorm_dw_kernel(const float* __restrict__ dw_part, float* __restrict__ dw,
+                                                         int nparts, int H) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  float s = 0.f;
+  for (int b = 0; b < nparts; ++b) s += dw_part[static_cast<int64_t>(b) * H + c];
+  dw[c] = s;
+}
+
+int32_t check_norm(const void* x, const void* w, const void* a, const void* b, int32_t T, int32_t H, int32_t dtype) {
+  if (x == nullptr || w == nullptr || a == nullptr || b == nullptr) return SSA_OPS_ERR_NULL_POINTER;
+  if (T <= 0 || H <= 0 || H % 4 != 0 || H > 4 * 4 * kNormThreads) return SSA_OPS_ERR_SHAPE;
+  if (dtype != 0 && dtype != 1 && dtype != 2) return SSA_OPS_ERR_DTYPE;
+  if (!aligned(x, 16) || !aligned(w, 16)) return SSA_OPS_ERR_ALIGNMENT;
+  return SSA_OPS_OK;
+}
+
 }  // namespace
 
 extern "C" int32_t ssa_rope(const ssa_rope_args* a, void* stream) {
@@ -94,4 +215,55 @@ extern "C" int32_t ssa_rope(const ssa_rope_args* a, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const hipError_t e = a->dtype == 0 ? launch_rope<__bf16>(a, st) : launch_rope<_Float16>(a, st);
   return e == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
+}
+
+extern "C" int64_t ssa_rmsnorm_workspace_floats(int32_t rows, int32_t hidden) {
+  if (rows <= 0 || hidden <= 0) return 0;
+  return static_cast<int64_t>((rows + kNormBwdRows - 1) / kNormBwdRows) * hidden;
+}
+
+extern "C" int32_t ssa_rmsnorm_fwd(const ssa_rmsnorm_fwd_args* a, void* stream) {
+  if (a == nullptr) return SSA_OPS_ERR_NULL_POINTER;
+  const int32_t st = check_norm(a->x, a->weight, a->y, a->rstd, a->rows, a->hidden, a->out_dtype);
+  if (st != SSA_OPS_OK) return st;
+  if (!aligned(a->y, 8)) return SSA_OPS_ERR_ALIGNMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float* x = static_cast<const float*>(a->x);
+  const float* w = static_cast<const float*>(a->weight);
+  switch (a->out_dtype) {
+    case 0: hipLaunchKernelGGL(rmsnorm_fwd_kernel<__bf16>, dim3(a->rows), dim3(kNormThreads), 0, s, x, w,
+                               static_cast<__bf16*>(a->y), a->rstd, a->hidden, a->eps); break;
+    case 1: hipLaunchKernelGGL(rmsnorm_fwd_kernel<_Float16>, dim3(a->rows), dim3(kNormThreads), 0, s, x, w,
+                               static_cast<_Float16*>(a->y), a->rstd, a->hidden, a->eps); break;
+    default: hipLaunchKernelGGL(rmsnorm_fwd_kernel<float>, dim3(a->rows), dim3(kNormThreads), 0, s, x, w,
+                                static_cast<float*>(a->y), a->rstd, a->hidden, a->eps); break;
+  }
+  return hipGetLastError() == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
+}
+
+extern "C" int32_t ssa_rmsnorm_bwd(const ssa_rmsnorm_bwd_args* a, void* stream) {
+  if (a == nullptr) return SSA_OPS_ERR_NULL_POINTER;
+  const int32_t st = check_norm(a->x, a->weight, a->dy, a->rstd, a->rows, a->hidden, a->dy_dtype);
+  if (st != SSA_OPS_OK) return st;
+  if (a->dx == nullptr || a->dweight == nullptr || a->workspace == nullptr) return SSA_OPS_ERR_NULL_POINTER;
+  if (!aligned(a->dx, 16) || !aligned(a->workspace, 16) || !aligned(a->dy, 8)) return SSA_OPS_ERR_ALIGNMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nparts = (a->rows + kNormBwdRows - 1) / kNormBwdRows;
+  const float* x = static_cast<const float*>(a->x);
+  const float* w = static_cast<const float*>(a->weight);
+  switch (a->dy_dtype) {
+    case 0: hipLaunchKernelGGL(rmsnorm_bwd_kernel<__bf16>, dim3(nparts), dim3(kNormThreads), 0, s, x, w,
+                               static_cast<const __bf16*>(a->dy), a->rstd, a->dx, a->workspace, a->rows,
+                               a->hidden); break;
+    case 1: hipLaunchKernelGGL(rmsnorm_bwd_kernel<_Float16>, dim3(nparts), dim3(kNormThreads), 0, s, x, w,
+                               static_cast<const _Float16*>(a->dy), a->rstd, a->dx, a->workspace, a->rows,
+                               a->hidden); break;
+    default: hipLaunchKernelGGL(rmsnorm_bwd_kernel<float>, dim3(nparts), dim3(kNormThreads), 0, s, x, w,
+                                static_cast<const float*>(a->dy), a->rstd, a->dx, a->workspace, a->rows,
+                                a->hidden); break;
+  }
+  if (hipGetLastError() != hipSuccess) return SSA_OPS_ERR_LAUNCH;
+  hipLaunchKernelGGL(rmsnorm_dw_kernel, dim3((a->hidden + 255) / 256), dim3(256), 0, s, a->workspace, a->dweight,
+                     nparts, a->hidden);
+  return hipGetLastError() == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
 }

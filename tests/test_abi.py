@@ -304,3 +304,24 @@ def test_rope_validation(field, value, status):
     """ssa_rope (include/ssa_decoder_ops.h) rejects bad arguments on the host."""
     a = _rope_args(**{field: value})
     assert _lib.lib().ssa_rope(ctypes.byref(a), None) == status
+
+
+
+def test_rmsnorm_validation_and_workspace():
+    """ssa_rmsnorm_* (include/ssa_decoder_ops.h) reject bad arguments on the host."""
+    lib = _lib.lib()
+    assert lib.ssa_rmsnorm_workspace_floats(16384, 2048) == 256 * 2048
+    assert lib.ssa_rmsnorm_workspace_floats(65, 8) == 2 * 8
+    assert lib.ssa_rmsnorm_workspace_floats(0, 8) == 0
+    f = _lib.RmsNormFwdArgs(FAKE, FAKE, FAKE, FAKE, 4, 2048, 0, 1e-5)
+    for field, value, status in (("x", None, 1), ("rows", 0, 2), ("hidden", 4100, 2), ("hidden", 6, 2),
+                                 ("out_dtype", 3, 3), ("x", FAKE + 8, 4), ("y", FAKE + 2, 4)):
+        a = _lib.RmsNormFwdArgs(FAKE, FAKE, FAKE, FAKE, 4, 2048, 0, 1e-5)
+        setattr(a, field, value)
+        assert lib.ssa_rmsnorm_fwd(ctypes.byref(a), None) == status, field
+    for field, value, status in (("dy", None, 1), ("dx", None, 1), ("workspace", None, 1), ("hidden", 0, 2),
+                                 ("dy_dtype", 5, 3), ("dx", FAKE + 4, 4)):
+        a = _lib.RmsNormBwdArgs(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 2048, 0)
+        setattr(a, field, value)
+        assert lib.ssa_rmsnorm_bwd(ctypes.byref(a), None) == status, field
+    assert f.hidden == 2048

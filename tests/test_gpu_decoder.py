@@ -152,14 +152,14 @@ def test_fused_rope_matches_torch(gpu, D, dtype):
     assert ((ga - gb).abs() <= 2 * tol * pair_norm(gb) + 1e-6).all()
 
 
-def test_decoder_fused_rope_equals_torch_rope(gpu):
-    """The same decoder with the fused RoPE kernel and with the PyTorch form:
-    logits and gradients agree to bf16-level relative error."""
+def test_decoder_fused_ops_equal_torch_ops(gpu):
+    """The same decoder with the fused RoPE and RMSNorm kernels and with the
+    PyTorch forms: logits and gradients agree to bf16-level relative error."""
     import dataclasses
 
     from SSA.ssa_decoder import SSADecoder
 
-    print("[gpu case] decoder fused vs torch RoPE", file=sys.stderr, flush=True)
+    print("[gpu case] decoder fused vs torch RoPE / RMSNorm", file=sys.stderr, flush=True)
     torch.manual_seed(4)
     cfg = _tiny(True)
     model = SSADecoder(cfg).to(gpu)
@@ -168,6 +168,9 @@ def test_decoder_fused_rope_equals_torch_rope(gpu):
 
     def run(fused):
         model.cfg = dataclasses.replace(cfg, fused_rope=fused)
+        for mod in model.modules():
+            if hasattr(mod, "fused"):
+                mod.fused = fused  # RMSNorm
         model.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.bfloat16):
             logits = model(ids)
@@ -181,3 +184,36 @@ def test_decoder_fused_rope_equals_torch_rope(gpu):
     assert _rel(la, lb) <= 1e-2, _rel(la, lb)
     for name in ga:
         assert _rel(ga[name], gb[name]) <= 3e-2, (name, _rel(ga[name], gb[name]))
+
+
+@pytest.mark.parametrize("autocast", [True, False])
+def test_fused_rmsnorm_matches_torch(gpu, autocast):
+    """ssa_rmsnorm_fwd / _bwd against the PyTorch form in fp32: the output in
+    the autocast dtype (bf16) or fp32, dx and the weight gradient (a sum over
+    all rows, reduced in a fixed order)."""
+    from SSA.ssa_decoder import RMSNorm
+
+    print(f"[gpu case] fused RMSNorm autocast={autocast}", file=sys.stderr, flush=True)
+    torch.manual_seed(5)
+    S, B, H = 513, 3, 2048
+    norm = RMSNorm(H, 1e-5).to(gpu)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(H, device=gpu))
+    x = torch.randn(S, B, H, device=gpu) * 3
+    up = torch.randn(S, B, H, device=gpu)
+    xa = x.clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        ya = norm(xa)
+    (ya.float() * up).sum().backward()
+    ga_x, ga_w = xa.grad.clone(), norm.weight.grad.clone()
+    norm.weight.grad = None
+    xb = x.clone().requires_grad_(True)
+    yb = norm.reference(xb)
+    dy = up.to(ya.dtype).float()  # the upstream gradient as the fused backward sees it
+    (yb * dy).sum().backward()
+    torch.cuda.synchronize()
+    assert ya.dtype == (torch.bfloat16 if autocast else torch.float32)
+    tol = 2.0 ** -8 if autocast else 1e-5
+    assert ((ya.float() - yb).abs() <= tol * yb.abs() + 1e-5).all()
+    assert _rel(ga_x, xb.grad) <= 1e-4, _rel(ga_x, xb.grad)
+    assert _rel(ga_w, norm.weight.grad) <= 1e-4, _rel(ga_w, norm.weight.grad)
