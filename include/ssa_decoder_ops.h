@@ -92,6 +92,28 @@ int64_t ssa_rmsnorm_workspace_floats(int32_t rows, int32_t hidden);
 int32_t ssa_rmsnorm_fwd(const ssa_rmsnorm_fwd_args* args, void* stream);
 int32_t ssa_rmsnorm_bwd(const ssa_rmsnorm_bwd_args* args, void* stream);
 
+/*
+ * SwiGLU gate of the MLP: h = silu(gate) * up, where z = [gate | up] is the
+ * fc1 output, rows of 2 * ffn values.  Replaces the gated-linear-unit
+ * activation of the Megatron MLP in the reference's SSA layer spec
+ * (training/train/train_ssa_triton/SSA/ssa_triton_layer_specs.py:96-127;
+ * "swiglu" in the run configuration).
+ *
+ * backward = 0: out = h [rows, ffn].  backward = 1: dh [rows, ffn] in, out =
+ * dz [rows, 2 * ffn] = [d gate | d up].  bf16 or fp16, contiguous, 8-byte
+ * aligned; ffn a multiple of 4.  fp32 math, one rounding per output.
+ */
+typedef struct {
+  const void* z;
+  const void* dh;
+  void* out;
+  int32_t rows, ffn;
+  int32_t dtype; /* 0 = bf16, 1 = fp16 */
+  int32_t backward;
+} ssa_swiglu_args;
+
+int32_t ssa_swiglu(const ssa_swiglu_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "ssa_rmsnorm_workspace_floats",
     "ssa_rmsnorm_fwd",
     "ssa_rmsnorm_bwd",
+    "ssa_swiglu",
 )
 
 ABI_VERSION = 4
@@ -163,6 +164,20 @@ class RmsNormBwdArgs(ctypes.Structure):
     ]
 
 
+class SwigluArgs(ctypes.Structure):
+    """ssa_swiglu_args of include/ssa_decoder_ops.h."""
+
+    _fields_ = [
+        ("z", ctypes.c_void_p),
+        ("dh", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("ffn", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("backward", ctypes.c_int32),
+    ]
+
+
 class VarlenFwdArgs(ctypes.Structure):
     _fields_ = [("dense", FwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
 
@@ -215,7 +230,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
     for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs),
                        ("ssa_decode", DecodeArgs), ("ssa_rope", RopeArgs), ("ssa_rmsnorm_fwd", RmsNormFwdArgs),
-                       ("ssa_rmsnorm_bwd", RmsNormBwdArgs)):
+                       ("ssa_rmsnorm_bwd", RmsNormBwdArgs), ("ssa_swiglu", SwigluArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]

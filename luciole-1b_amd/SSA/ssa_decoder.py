@@ -53,6 +53,7 @@ class SSADecoderConfig:
     init_std: float = 0.02
     fused_rope: bool = True  # ssa_rope on the GPU (False: the PyTorch form)
     fused_norm: bool = True  # ssa_rmsnorm_* on the GPU (False: the PyTorch form)
+    fused_swiglu: bool = True  # ssa_swiglu on the GPU (False: the PyTorch form)
 
     def num_parameters(self) -> int:
         h, f, v = self.hidden_size, self.ffn_hidden_size, self.vocab_size
@@ -219,14 +220,49 @@ class SelfAttention(nn.Module):
         return self.linear_proj(ctx)
 
 
+def _swiglu_launch(z, dh, backward: bool):
+    from . import _lib
+
+    F2 = z.shape[-1]
+    rows = z.numel() // F2
+    shape = z.shape[:-1] + ((F2,) if backward else (F2 // 2,))
+    out = torch.empty(shape, device=z.device, dtype=z.dtype)
+    args = _lib.SwigluArgs(z.data_ptr(), dh.data_ptr() if dh is not None else None, out.data_ptr(), rows, F2 // 2,
+                           0 if z.dtype == torch.bfloat16 else 1, int(backward))
+    with torch.cuda.device(z.device):
+        stream = torch.cuda.current_stream(z.device).cuda_stream
+        _lib.check(_lib.lib().ssa_swiglu(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_swiglu")
+    return out
+
+
+class FusedSwiGLU(torch.autograd.Function):
+    """silu(gate) * up of z = [gate | up] (the fc1 output) as one HIP pass each
+    way (``ssa_swiglu``); the backward writes both halves of dz directly."""
+
+    @staticmethod
+    def forward(ctx, z):
+        z = z.contiguous()
+        ctx.save_for_backward(z)
+        return _swiglu_launch(z, None, False)
+
+    @staticmethod
+    def backward(ctx, dh):
+        (z,) = ctx.saved_tensors
+        return _swiglu_launch(z, dh.contiguous(), True)
+
+
 class MLP(nn.Module):
     def __init__(self, cfg: SSADecoderConfig):
         super().__init__()
         self.linear_fc1 = nn.Linear(cfg.hidden_size, 2 * cfg.ffn_hidden_size, bias=False)  # [gate; up]
         self.linear_fc2 = nn.Linear(cfg.ffn_hidden_size, cfg.hidden_size, bias=False)
+        self.fused = cfg.fused_swiglu
 
     def forward(self, x):
-        gate, up = self.linear_fc1(x).chunk(2, dim=-1)
+        z = self.linear_fc1(x)
+        if self.fused and z.is_cuda and z.dtype in (torch.bfloat16, torch.float16) and z.shape[-1] % 8 == 0:
+            return self.linear_fc2(FusedSwiGLU.apply(z))
+        gate, up = z.chunk(2, dim=-1)
         return self.linear_fc2(F.silu(gate) * up)
 
 

@@ -1,7 +1,8 @@
 // Fused element-wise operators of the SSA decoder layer around the attention
 // path (gfx950): rotary position embedding (one HBM pass per call in the
-// input dtype; the unfused PyTorch form makes six fp32 passes) and RMSNorm
-// (one pass forward, one backward, plus a fixed-order weight-gradient sum).
+// input dtype; the unfused PyTorch form makes six fp32 passes), RMSNorm
+// (one pass forward, one backward, plus a fixed-order weight-gradient sum)
+// and the SwiGLU gate (one pass each way).
 //
 // Rotate-half RoPE (Megatron's default, non-interleaved), per (s, b, h) row of
 // D values, i < D / 2, with c = cos[s][i], t = sin[s][i]:
@@ -191,6 +192,47 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_kernel(const float* __restrict
   dw[c] = s;
 }
 
+// ---------------------------------------------------------------------------
+// SwiGLU of the MLP: z = [gate | up] rows of 2F values (the fc1 output), h =
+// silu(gate) up with silu(g) = g sigmoid(g), in fp32, rounded once.
+// Backward from dh: with s = sigmoid(g), d_up = dh silu(g) and
+// d_gate = dh up s (1 + g (1 - s)), written as the [d_gate | d_up] rows of dz.
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ z, const T* __restrict__ dh,
+                                                     T* __restrict__ out, int64_t T_rows, int F, int backward) {
+  typedef typename Pack4<T>::type v4;
+  const int q = F / 4;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= T_rows * q) return;
+  const int64_t row = gid / q;
+  const int c = static_cast<int>(gid % q) * 4;
+  const T* zr = z + row * 2 * F;
+  const v4 g = *reinterpret_cast<const v4*>(zr + c);
+  const v4 u = *reinterpret_cast<const v4*>(zr + F + c);
+  if (!backward) {
+    v4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float gf = static_cast<float>(g[e]);
+      h[e] = static_cast<T>(gf / (1.f + __expf(-gf)) * static_cast<float>(u[e]));
+    }
+    *reinterpret_cast<v4*>(out + row * F + c) = h;
+  } else {
+    const v4 d = *reinterpret_cast<const v4*>(dh + row * F + c);
+    v4 dg, du;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float gf = static_cast<float>(g[e]), uf = static_cast<float>(u[e]), df = static_cast<float>(d[e]);
+      const float sg = 1.f / (1.f + __expf(-gf));
+      du[e] = static_cast<T>(df * gf * sg);
+      dg[e] = static_cast<T>(df * uf * sg * (1.f + gf * (1.f - sg)));
+    }
+    T* orow = out + row * 2 * F;
+    *reinterpret_cast<v4*>(orow + c) = dg;
+    *reinterpret_cast<v4*>(orow + F + c) = du;
+  }
+}
+
 int32_t check_norm(const void* x, const void* w, const void* a, const void* b, int32_t T, int32_t H, int32_t dtype) {
   if (x == nullptr || w == nullptr || a == nullptr || b == nullptr) return SSA_OPS_ERR_NULL_POINTER;
   if (T <= 0 || H <= 0 || H % 4 != 0 || H > 4 * 4 * kNormThreads) return SSA_OPS_ERR_SHAPE;
@@ -265,5 +307,25 @@ extern "C" int32_t ssa_rmsnorm_bwd(const ssa_rmsnorm_bwd_args* a, void* stream) 
   if (hipGetLastError() != hipSuccess) return SSA_OPS_ERR_LAUNCH;
   hipLaunchKernelGGL(rmsnorm_dw_kernel, dim3((a->hidden + 255) / 256), dim3(256), 0, s, a->workspace, a->dweight,
                      nparts, a->hidden);
+  return hipGetLastError() == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
+}
+
+extern "C" int32_t ssa_swiglu(const ssa_swiglu_args* a, void* stream) {
+  if (a == nullptr || a->z == nullptr || a->out == nullptr || (a->backward && a->dh == nullptr))
+    return SSA_OPS_ERR_NULL_POINTER;
+  if (a->rows <= 0 || a->ffn <= 0 || a->ffn % 4 != 0) return SSA_OPS_ERR_SHAPE;
+  if (a->dtype != 0 && a->dtype != 1) return SSA_OPS_ERR_DTYPE;
+  if (!aligned(a->z, 8) || !aligned(a->out, 8) || (a->backward && !aligned(a->dh, 8))) return SSA_OPS_ERR_ALIGNMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t threads = static_cast<int64_t>(a->rows) * (a->ffn / 4);
+  const int grid = static_cast<int>((threads + 255) / 256);
+  if (a->dtype == 0)
+    hipLaunchKernelGGL(swiglu_kernel<__bf16>, dim3(grid), dim3(256), 0, s, static_cast<const __bf16*>(a->z),
+                       static_cast<const __bf16*>(a->dh), static_cast<__bf16*>(a->out), static_cast<int64_t>(a->rows),
+                       a->ffn, a->backward);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<_Float16>, dim3(grid), dim3(256), 0, s, static_cast<const _Float16*>(a->z),
+                       static_cast<const _Float16*>(a->dh), static_cast<_Float16*>(a->out),
+                       static_cast<int64_t>(a->rows), a->ffn, a->backward);
   return hipGetLastError() == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
 }

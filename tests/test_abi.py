@@ -325,3 +325,15 @@ def test_rmsnorm_validation_and_workspace():
         setattr(a, field, value)
         assert lib.ssa_rmsnorm_bwd(ctypes.byref(a), None) == status, field
     assert f.hidden == 2048
+
+
+def test_swiglu_validation():
+    """ssa_swiglu (include/ssa_decoder_ops.h) rejects bad arguments on the host."""
+    lib = _lib.lib()
+    for field, value, status in (("z", None, 1), ("out", None, 1), ("rows", 0, 2), ("ffn", 6, 2),
+                                 ("dtype", 2, 3), ("z", FAKE + 4, 4)):
+        a = _lib.SwigluArgs(FAKE, None, FAKE, 4, 64, 0, 0)
+        setattr(a, field, value)
+        assert lib.ssa_swiglu(ctypes.byref(a), None) == status, field
+    a = _lib.SwigluArgs(FAKE, None, FAKE, 4, 64, 0, 1)  # backward needs dh
+    assert lib.ssa_swiglu(ctypes.byref(a), None) == 1

@@ -153,8 +153,8 @@ def test_fused_rope_matches_torch(gpu, D, dtype):
 
 
 def test_decoder_fused_ops_equal_torch_ops(gpu):
-    """The same decoder with the fused RoPE and RMSNorm kernels and with the
-    PyTorch forms: logits and gradients agree to bf16-level relative error."""
+    """The same decoder with the fused RoPE, RMSNorm and SwiGLU kernels and with
+    the PyTorch forms: logits and gradients agree to bf16-level relative error."""
     import dataclasses
 
     from SSA.ssa_decoder import SSADecoder
@@ -170,7 +170,7 @@ def test_decoder_fused_ops_equal_torch_ops(gpu):
         model.cfg = dataclasses.replace(cfg, fused_rope=fused)
         for mod in model.modules():
             if hasattr(mod, "fused"):
-                mod.fused = fused  # RMSNorm
+                mod.fused = fused  # RMSNorm, MLP (SwiGLU)
         model.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.bfloat16):
             logits = model(ids)
@@ -217,3 +217,26 @@ def test_fused_rmsnorm_matches_torch(gpu, autocast):
     assert ((ya.float() - yb).abs() <= tol * yb.abs() + 1e-5).all()
     assert _rel(ga_x, xb.grad) <= 1e-4, _rel(ga_x, xb.grad)
     assert _rel(ga_w, norm.weight.grad) <= 1e-4, _rel(ga_w, norm.weight.grad)
+
+
+def test_fused_swiglu_matches_torch(gpu):
+    """ssa_swiglu against silu(gate) * up in fp32, forward and backward (both
+    halves of the fc1 gradient): within bf16 rounding."""
+    from SSA.ssa_decoder import FusedSwiGLU
+
+    print("[gpu case] fused SwiGLU", file=sys.stderr, flush=True)
+    torch.manual_seed(6)
+    z = (torch.randn(700, 3, 2 * 5632, device=gpu) * 2).to(torch.bfloat16)
+    za = z.clone().requires_grad_(True)
+    zb = z.float().requires_grad_(True)
+    ha = FusedSwiGLU.apply(za)
+    g, u = zb.chunk(2, dim=-1)
+    hb = torch.nn.functional.silu(g) * u
+    w = torch.randn_like(hb)
+    (ha.float() * w).sum().backward()
+    (hb * w.to(torch.bfloat16).float()).sum().backward()
+    torch.cuda.synchronize()
+    tol = 2.0 ** -8
+    assert ((ha.float() - hb).abs() <= tol * hb.abs() + 1e-4).all()
+    ga, gb = za.grad.float(), zb.grad
+    assert ((ga - gb).abs() <= 2 * tol * gb.abs() + 1e-3).all()
