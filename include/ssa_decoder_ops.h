@@ -114,6 +114,34 @@ typedef struct {
 
 int32_t ssa_swiglu(const ssa_swiglu_args* args, void* stream);
 
+/*
+ * Cross-entropy of the output layer's logits against integer labels, the
+ * loss of the reference's training step (Megatron's GPT loss over the vocab
+ * logits; the reference runs it through its layer spec,
+ * training/train/train_ssa_triton/SSA/ssa_triton_layer_specs.py:96-127).
+ *
+ * logits [rows, vocab] bf16/fp16 contiguous, 8-byte aligned, vocab a
+ * multiple of 4; labels int64 [rows], a row with a label outside [0, vocab)
+ * is ignored (loss 0, gradient 0).  Forward (backward = 0): loss [rows] fp32
+ * per row (log-sum-exp minus the label's logit) and lse [rows] fp32, kept for
+ * the backward.  Backward (backward = 1): dlogits [rows, vocab] in the logits'
+ * dtype = (softmax - one-hot) * scale[0], scale a device fp32 scalar (the
+ * upstream gradient over the number of counted rows for a mean).
+ */
+typedef struct {
+  const void* logits;
+  const void* labels;
+  float* loss;
+  float* lse;
+  const float* scale;
+  void* dlogits;
+  int32_t rows, vocab;
+  int32_t dtype; /* 0 = bf16, 1 = fp16 */
+  int32_t backward;
+} ssa_cross_entropy_args;
+
+int32_t ssa_cross_entropy(const ssa_cross_entropy_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

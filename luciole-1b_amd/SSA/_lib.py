@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "ssa_rmsnorm_fwd",
     "ssa_rmsnorm_bwd",
     "ssa_swiglu",
+    "ssa_cross_entropy",
 )
 
 ABI_VERSION = 4
@@ -178,6 +179,23 @@ class SwigluArgs(ctypes.Structure):
     ]
 
 
+class CrossEntropyArgs(ctypes.Structure):
+    """ssa_cross_entropy_args of include/ssa_decoder_ops.h."""
+
+    _fields_ = [
+        ("logits", ctypes.c_void_p),
+        ("labels", ctypes.c_void_p),
+        ("loss", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("dlogits", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("backward", ctypes.c_int32),
+    ]
+
+
 class VarlenFwdArgs(ctypes.Structure):
     _fields_ = [("dense", FwdArgs), ("cu_seqlens", ctypes.c_void_p), ("total_tokens", ctypes.c_int32)]
 
@@ -230,7 +248,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
     for name, argt in (("ssa_varlen_fwd", VarlenFwdArgs), ("ssa_varlen_bwd", VarlenBwdArgs),
                        ("ssa_decode", DecodeArgs), ("ssa_rope", RopeArgs), ("ssa_rmsnorm_fwd", RmsNormFwdArgs),
-                       ("ssa_rmsnorm_bwd", RmsNormBwdArgs), ("ssa_swiglu", SwigluArgs)):
+                       ("ssa_rmsnorm_bwd", RmsNormBwdArgs), ("ssa_swiglu", SwigluArgs),
+                       ("ssa_cross_entropy", CrossEntropyArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]

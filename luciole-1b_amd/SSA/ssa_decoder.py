@@ -54,6 +54,7 @@ class SSADecoderConfig:
     fused_rope: bool = True  # ssa_rope on the GPU (False: the PyTorch form)
     fused_norm: bool = True  # ssa_rmsnorm_* on the GPU (False: the PyTorch form)
     fused_swiglu: bool = True  # ssa_swiglu on the GPU (False: the PyTorch form)
+    fused_loss: bool = True  # ssa_cross_entropy on the GPU (False: F.cross_entropy on fp32 logits)
 
     def num_parameters(self) -> int:
         h, f, v = self.hidden_size, self.ffn_hidden_size, self.vocab_size
@@ -251,6 +252,52 @@ class FusedSwiGLU(torch.autograd.Function):
         return _swiglu_launch(z, dh.contiguous(), True)
 
 
+class FusedCrossEntropy(torch.autograd.Function):
+    """Mean cross-entropy of bf16/fp16 logits [rows, vocab] against int64 labels
+    (``ssa_cross_entropy``): one pass over the logits each way, no fp32 copy;
+    labels outside [0, vocab) (e.g. -100) are ignored, as by
+    ``F.cross_entropy``."""
+
+    @staticmethod
+    def _launch(args):
+        from . import _lib
+
+        with torch.cuda.device(torch.cuda.current_device()):
+            stream = torch.cuda.current_stream().cuda_stream
+            _lib.check(_lib.lib().ssa_cross_entropy(ctypes.byref(args), ctypes.c_void_p(stream)), "ssa_cross_entropy")
+
+    @staticmethod
+    def forward(ctx, logits, labels):
+        from . import _lib
+
+        logits = logits.contiguous()
+        labels = labels.to(torch.int64).contiguous()
+        R, V = logits.shape
+        loss = torch.empty(R, device=logits.device, dtype=torch.float32)
+        lse = torch.empty(R, device=logits.device, dtype=torch.float32)
+        dt = 0 if logits.dtype == torch.bfloat16 else 1
+        with torch.cuda.device(logits.device):
+            FusedCrossEntropy._launch(_lib.CrossEntropyArgs(logits.data_ptr(), labels.data_ptr(), loss.data_ptr(),
+                                                            lse.data_ptr(), None, None, R, V, dt, 0))
+        n = ((labels >= 0) & (labels < V)).sum().clamp_min(1).to(torch.float32)
+        ctx.save_for_backward(logits, labels, lse, n)
+        return loss.sum() / n
+
+    @staticmethod
+    def backward(ctx, g):
+        from . import _lib
+
+        logits, labels, lse, n = ctx.saved_tensors
+        R, V = logits.shape
+        scale = (g.to(torch.float32) / n).reshape(()).contiguous()
+        dlogits = torch.empty_like(logits)
+        dt = 0 if logits.dtype == torch.bfloat16 else 1
+        with torch.cuda.device(logits.device):
+            FusedCrossEntropy._launch(_lib.CrossEntropyArgs(logits.data_ptr(), labels.data_ptr(), None, lse.data_ptr(),
+                                                            scale.data_ptr(), dlogits.data_ptr(), R, V, dt, 1))
+        return dlogits, None
+
+
 class MLP(nn.Module):
     def __init__(self, cfg: SSADecoderConfig):
         super().__init__()
@@ -321,7 +368,10 @@ class SSADecoder(nn.Module):
 
     def loss(self, input_ids, labels):
         logits = self(input_ids)  # [S, B, V]
-        return F.cross_entropy(logits.float().view(-1, logits.shape[-1]), labels.t().reshape(-1))
+        V = logits.shape[-1]
+        if self.cfg.fused_loss and logits.is_cuda and logits.dtype in (torch.bfloat16, torch.float16) and V % 4 == 0:
+            return FusedCrossEntropy.apply(logits.view(-1, V), labels.t().reshape(-1))
+        return F.cross_entropy(logits.float().view(-1, V), labels.t().reshape(-1))
 
     def new_caches(self, batch: int, capacity: int, dtype=torch.bfloat16) -> List[SSAKVCache]:
         dev = self.embedding.weight.device

@@ -1,8 +1,9 @@
 // Fused element-wise operators of the SSA decoder layer around the attention
 // path (gfx950): rotary position embedding (one HBM pass per call in the
 // input dtype; the unfused PyTorch form makes six fp32 passes), RMSNorm
-// (one pass forward, one backward, plus a fixed-order weight-gradient sum)
-// and the SwiGLU gate (one pass each way).
+// (one pass forward, one backward, plus a fixed-order weight-gradient sum),
+// the SwiGLU gate (one pass each way) and the output layer's cross-entropy
+// (one pass over the logits each way, no fp32 copy of them).
 //
 // Rotate-half RoPE (Megatron's default, non-interleaved), per (s, b, h) row of
 // D values, i < D / 2, with c = cos[s][i], t = sin[s][i]:
@@ -233,6 +234,71 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ z, co
   }
 }
 
+// ---------------------------------------------------------------------------
+// Cross-entropy over rows of V logits (bf16/fp16), one workgroup per row.
+// Forward: lse = log sum exp (one pass, running max per thread, merged across
+// the workgroup); loss = lse - logit[label] (0 for label < 0).  Backward:
+// dlogit = (exp(logit - lse) - [v == label]) * scale, 0 for an ignored row.
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+  const float mm = fmaxf(m, m2);
+  s = (m == -INFINITY ? 0.f : s * __expf(m - mm)) + (m2 == -INFINITY ? 0.f : s2 * __expf(m2 - mm));
+  m = mm;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void xent_fwd_kernel(const T* __restrict__ logits, const int64_t* __restrict__ labels,
+                                                       float* __restrict__ loss, float* __restrict__ lse, int V) {
+  typedef typename Pack4<T>::type v4;
+  __shared__ float sm[4], ss[4];
+  const int64_t row = blockIdx.x;
+  const T* lr = logits + row * V;
+  float m = -INFINITY, s = 0.f;
+  for (int c = threadIdx.x * 4; c < V; c += 256 * 4) {
+    const v4 x = *reinterpret_cast<const v4*>(lr + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lse_merge(m, s, static_cast<float>(x[e]), 1.f);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lse_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sm[wave] = m;
+    ss[wave] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = sm[0], S = ss[0];
+    for (int w = 1; w < 4; ++w) lse_merge(M, S, sm[w], ss[w]);
+    const float l = M + __logf(S);
+    lse[row] = l;
+    const int64_t lab = labels[row];
+    loss[row] = (lab >= 0 && lab < V) ? l - static_cast<float>(lr[lab]) : 0.f;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void xent_bwd_kernel(const T* __restrict__ logits, const int64_t* __restrict__ labels,
+                                                       const float* __restrict__ lse, const float* __restrict__ scale,
+                                                       T* __restrict__ dlogits, int V) {
+  typedef typename Pack4<T>::type v4;
+  const int64_t row = blockIdx.x;
+  const int64_t lab = labels[row];
+  const bool valid = lab >= 0 && lab < V;
+  const float l = lse[row], g = valid ? *scale : 0.f;
+  const T* lr = logits + row * V;
+  T* dr = dlogits + row * V;
+  for (int c = threadIdx.x * 4; c < V; c += 256 * 4) {
+    const v4 x = *reinterpret_cast<const v4*>(lr + c);
+    v4 d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __expf(static_cast<float>(x[e]) - l) - (c + e == lab ? 1.f : 0.f);
+      d[e] = static_cast<T>(p * g);
+    }
+    *reinterpret_cast<v4*>(dr + c) = d;
+  }
+}
+
 int32_t check_norm(const void* x, const void* w, const void* a, const void* b, int32_t T, int32_t H, int32_t dtype) {
   if (x == nullptr || w == nullptr || a == nullptr || b == nullptr) return SSA_OPS_ERR_NULL_POINTER;
   if (T <= 0 || H <= 0 || H % 4 != 0 || H > 4 * 4 * kNormThreads) return SSA_OPS_ERR_SHAPE;
@@ -327,5 +393,34 @@ extern "C" int32_t ssa_swiglu(const ssa_swiglu_args* a, void* stream) {
     hipLaunchKernelGGL(swiglu_kernel<_Float16>, dim3(grid), dim3(256), 0, s, static_cast<const _Float16*>(a->z),
                        static_cast<const _Float16*>(a->dh), static_cast<_Float16*>(a->out),
                        static_cast<int64_t>(a->rows), a->ffn, a->backward);
+  return hipGetLastError() == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
+}
+
+extern "C" int32_t ssa_cross_entropy(const ssa_cross_entropy_args* a, void* stream) {
+  if (a == nullptr || a->logits == nullptr || a->labels == nullptr || a->lse == nullptr) return SSA_OPS_ERR_NULL_POINTER;
+  if (!a->backward && a->loss == nullptr) return SSA_OPS_ERR_NULL_POINTER;
+  if (a->backward && (a->scale == nullptr || a->dlogits == nullptr)) return SSA_OPS_ERR_NULL_POINTER;
+  if (a->rows <= 0 || a->vocab <= 0 || a->vocab % 4 != 0) return SSA_OPS_ERR_SHAPE;
+  if (a->dtype != 0 && a->dtype != 1) return SSA_OPS_ERR_DTYPE;
+  if (!aligned(a->logits, 8) || (a->backward && !aligned(a->dlogits, 8))) return SSA_OPS_ERR_ALIGNMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t* lab = static_cast<const int64_t*>(a->labels);
+  if (!a->backward) {
+    if (a->dtype == 0)
+      hipLaunchKernelGGL(xent_fwd_kernel<__bf16>, dim3(a->rows), dim3(256), 0, s,
+                         static_cast<const __bf16*>(a->logits), lab, a->loss, a->lse, a->vocab);
+    else
+      hipLaunchKernelGGL(xent_fwd_kernel<_Float16>, dim3(a->rows), dim3(256), 0, s,
+                         static_cast<const _Float16*>(a->logits), lab, a->loss, a->lse, a->vocab);
+  } else {
+    if (a->dtype == 0)
+      hipLaunchKernelGGL(xent_bwd_kernel<__bf16>, dim3(a->rows), dim3(256), 0, s,
+                         static_cast<const __bf16*>(a->logits), lab, a->lse, a->scale,
+                         static_cast<__bf16*>(a->dlogits), a->vocab);
+    else
+      hipLaunchKernelGGL(xent_bwd_kernel<_Float16>, dim3(a->rows), dim3(256), 0, s,
+                         static_cast<const _Float16*>(a->logits), lab, a->lse, a->scale,
+                         static_cast<_Float16*>(a->dlogits), a->vocab);
+  }
   return hipGetLastError() == hipSuccess ? SSA_OPS_OK : SSA_OPS_ERR_LAUNCH;
 }

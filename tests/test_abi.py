@@ -337,3 +337,16 @@ def test_swiglu_validation():
         assert lib.ssa_swiglu(ctypes.byref(a), None) == status, field
     a = _lib.SwigluArgs(FAKE, None, FAKE, 4, 64, 0, 1)  # backward needs dh
     assert lib.ssa_swiglu(ctypes.byref(a), None) == 1
+
+
+
+def test_cross_entropy_validation():
+    """ssa_cross_entropy (include/ssa_decoder_ops.h) rejects bad arguments on the host."""
+    lib = _lib.lib()
+    for field, value, status in (("logits", None, 1), ("loss", None, 1), ("rows", 0, 2), ("vocab", 6, 2),
+                                 ("dtype", 2, 3), ("logits", FAKE + 2, 4)):
+        a = _lib.CrossEntropyArgs(FAKE, FAKE, FAKE, FAKE, None, None, 4, 64, 0, 0)
+        setattr(a, field, value)
+        assert lib.ssa_cross_entropy(ctypes.byref(a), None) == status, field
+    a = _lib.CrossEntropyArgs(FAKE, FAKE, None, FAKE, None, FAKE, 4, 64, 0, 1)  # backward needs scale
+    assert lib.ssa_cross_entropy(ctypes.byref(a), None) == 1

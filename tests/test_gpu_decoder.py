@@ -240,3 +240,27 @@ def test_fused_swiglu_matches_torch(gpu):
     assert ((ha.float() - hb).abs() <= tol * hb.abs() + 1e-4).all()
     ga, gb = za.grad.float(), zb.grad
     assert ((ga - gb).abs() <= 2 * tol * gb.abs() + 1e-3).all()
+
+
+def test_fused_cross_entropy_matches_torch(gpu):
+    """ssa_cross_entropy against F.cross_entropy on the fp32 logits, with
+    ignored labels (-100): the mean loss and the logits gradient."""
+    from SSA.ssa_decoder import FusedCrossEntropy
+
+    print("[gpu case] fused cross-entropy", file=sys.stderr, flush=True)
+    torch.manual_seed(7)
+    R, V = 1000, 65536
+    logits = (torch.randn(R, V, device=gpu) * 4).to(torch.bfloat16)
+    labels = torch.randint(0, V, (R,), device=gpu)
+    labels[::7] = -100
+    la = logits.clone().requires_grad_(True)
+    lb = logits.float().requires_grad_(True)
+    loss_a = FusedCrossEntropy.apply(la, labels)
+    loss_b = torch.nn.functional.cross_entropy(lb, labels)
+    (loss_a * 3).backward()
+    (loss_b * 3).backward()
+    torch.cuda.synchronize()
+    assert abs(loss_a.item() - loss_b.item()) <= 1e-5 * abs(loss_b.item()), (loss_a.item(), loss_b.item())
+    ga, gb = la.grad.float(), lb.grad
+    assert ((ga - gb).abs() <= 2.0 ** -8 * gb.abs() + 1e-3 * gb.abs().max()).all()
+    assert (ga[::7] == 0).all()
