@@ -186,16 +186,17 @@ def test_decoder_fused_ops_equal_torch_ops(gpu):
         assert _rel(ga[name], gb[name]) <= 3e-2, (name, _rel(ga[name], gb[name]))
 
 
+@pytest.mark.parametrize("H", [2048, 1000, 4096])
 @pytest.mark.parametrize("autocast", [True, False])
-def test_fused_rmsnorm_matches_torch(gpu, autocast):
+def test_fused_rmsnorm_matches_torch(gpu, autocast, H):
     """ssa_rmsnorm_fwd / _bwd against the PyTorch form in fp32: the output in
     the autocast dtype (bf16) or fp32, dx and the weight gradient (a sum over
     all rows, reduced in a fixed order)."""
     from SSA.ssa_decoder import RMSNorm
 
-    print(f"[gpu case] fused RMSNorm autocast={autocast}", file=sys.stderr, flush=True)
+    print(f"[gpu case] fused RMSNorm autocast={autocast} H={H}", file=sys.stderr, flush=True)
     torch.manual_seed(5)
-    S, B, H = 513, 3, 2048
+    S, B = 513, 3
     norm = RMSNorm(H, 1e-5).to(gpu)
     with torch.no_grad():
         norm.weight.copy_(1 + 0.1 * torch.randn(H, device=gpu))
@@ -219,14 +220,15 @@ def test_fused_rmsnorm_matches_torch(gpu, autocast):
     assert _rel(ga_w, norm.weight.grad) <= 1e-4, _rel(ga_w, norm.weight.grad)
 
 
-def test_fused_swiglu_matches_torch(gpu):
+@pytest.mark.parametrize("F", [5632, 100])
+def test_fused_swiglu_matches_torch(gpu, F):
     """ssa_swiglu against silu(gate) * up in fp32, forward and backward (both
     halves of the fc1 gradient): within bf16 rounding."""
     from SSA.ssa_decoder import FusedSwiGLU
 
-    print("[gpu case] fused SwiGLU", file=sys.stderr, flush=True)
+    print(f"[gpu case] fused SwiGLU F={F}", file=sys.stderr, flush=True)
     torch.manual_seed(6)
-    z = (torch.randn(700, 3, 2 * 5632, device=gpu) * 2).to(torch.bfloat16)
+    z = (torch.randn(700, 3, 2 * F, device=gpu) * 2).to(torch.bfloat16)
     za = z.clone().requires_grad_(True)
     zb = z.float().requires_grad_(True)
     ha = FusedSwiGLU.apply(za)
@@ -242,14 +244,15 @@ def test_fused_swiglu_matches_torch(gpu):
     assert ((ga - gb).abs() <= 2 * tol * gb.abs() + 1e-3).all()
 
 
-def test_fused_cross_entropy_matches_torch(gpu):
+@pytest.mark.parametrize("V", [65536, 1000])
+def test_fused_cross_entropy_matches_torch(gpu, V):
     """ssa_cross_entropy against F.cross_entropy on the fp32 logits, with
     ignored labels (-100): the mean loss and the logits gradient."""
     from SSA.ssa_decoder import FusedCrossEntropy
 
-    print("[gpu case] fused cross-entropy", file=sys.stderr, flush=True)
+    print(f"[gpu case] fused cross-entropy V={V}", file=sys.stderr, flush=True)
     torch.manual_seed(7)
-    R, V = 1000, 65536
+    R = 1000
     logits = (torch.randn(R, V, device=gpu) * 4).to(torch.bfloat16)
     labels = torch.randint(0, V, (R,), device=gpu)
     labels[::7] = -100
