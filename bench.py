@@ -121,41 +121,69 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(S, D, causal, budget_s=20.0):
-    """Time the fp32 PyTorch-eager oracle on (b, h) slices of the workload on the host."""
+def _time_oracle(B, H, S, D, causal, runs, warmup, budget_s, seed=1234, qkv_scale=0.5):
+    """Median wall time of the fp32 torch oracle's fwd + autograd bwd on one
+    [B, H, S, D] problem (inputs drawn once, outside the timed region)."""
     import torch
 
     from oracle.ssa_oracle_torch import run_reference_grads
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(1234)
-    q = torch.randn(1, 1, S, D, generator=g) * 0.5
-    k = torch.randn(1, 1, S, D, generator=g) * 0.5
-    v = torch.randn(1, 1, S, D, generator=g) * 0.5
-    do = torch.randn(1, 1, S, D, generator=g)
-    n = torch.tensor(1.5)
-    b = torch.tensor(0.8)
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, H, S, D, generator=g) * qkv_scale for _ in range(3))
+    do = torch.randn(B, H, S, D, generator=g)
+    n, b = torch.tensor(1.5), torch.tensor(0.8)
     scale = 1.0 / math.sqrt(D)
-    run_reference_grads(q, k, v, scale, n, b, do, causal)  # warm-up
+    for _ in range(warmup):
+        run_reference_grads(q, k, v, scale, n, b, do, causal)
     times = []
     t_start = time.perf_counter()
-    while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
+    while len(times) < runs and (time.perf_counter() - t_start) < budget_s:
         t0 = time.perf_counter()
         run_reference_grads(q, k, v, scale, n, b, do, causal)
         times.append(time.perf_counter() - t0)
     times.sort()
-    med = times[len(times) // 2]
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(B, H, S, D, causal, budget_s=20.0):
+    """The fp32 PyTorch-eager oracle (oracle/ssa_oracle_torch.py, fwd + autograd
+    bwd) on the host cores, as a reported baseline:
+
+    * BASELINE.json configs[0] (B=1, H=4, S=256, D=64, fp32, causal; N(0,1)
+      inputs) timed in full: 3 warm-up runs, median of 10;
+    * the GPU workload timed on (b, h) slices -- one slice's S x S fp32
+      intermediates are what fit -- with the number of slices timed and the
+      whole step extrapolated as B * H slices.
+
+    ``value`` is the slice rate in the metric's unit (TFLOP/s of the same
+    14 D pairs count), i.e. the rate of the full step on these cores."""
+    import torch
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    c1_med, c1_runs = _time_oracle(1, 4, 256, 64, True, runs=10, warmup=3, budget_s=budget_s / 4, qkv_scale=1.0)
+    c1_flop = 14 * 64 * pairs_dense(1, 4, 256, True)
+    med, runs = _time_oracle(1, 1, S, D, causal, runs=10, warmup=1, budget_s=budget_s)
     flops = 14 * D * pairs_dense(1, 1, S, causal)
+    slices = B * H
+    model = cpu_model()
     return {
         "value": flops / med / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{len(times)} runs of one (b,h) slice S={S} D={D} fp32 causal={int(causal)} "
-                   f"fwd+autograd bwd, median {med * 1e3:.1f} ms; os.cpu_count()={threads}; "
-                   f"cpu={cpu_model()}"),
+        "sample": (f"{runs} runs of one (b,h) slice of the workload (S={S} D={D} fp32 causal={int(causal)}, "
+                   f"fwd+autograd bwd), median {med * 1e3:.1f} ms; the full step is {slices} such slices, "
+                   f"about {slices * med:.1f} s on these cores; os.cpu_count()={threads}; cpu={model}"),
         "ms_per_slice": med * 1e3,
+        "slices_timed": runs,
+        "slices_per_step": slices,
+        "full_step_s_extrapolated": slices * med,
+        "cpu_model": model,
+        "os_cpu_count": threads,
+        "config0": {"workload": "BASELINE.json configs[0]: B=1 H=4 S=256 D=64 fp32 causal, timed in full",
+                    "ms": c1_med * 1e3, "runs": c1_runs, "tflops": c1_flop / c1_med / 1e12,
+                    "alg_mflop": c1_flop / 1e6},
     }
 
 
@@ -333,7 +361,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(S, D, causal)
+        result["cpu_baseline"] = cpu_baseline(B, Hq, S, D, causal)
     print(json.dumps(result))
 
 

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 4
+#define SSA_ABI_VERSION 5
 
 /* Status codes. */
 enum {
@@ -173,7 +173,12 @@ int32_t ssa_bwd_reduce(const ssa_bwd_args* args, void* stream);
  * ssa_bwd_partials_count(batch, heads_kv, seqlen) floats.  The table is read
  * on the device only: entries are clamped to [0, total_tokens] and lengths to
  * seqlen, so a malformed table gives wrong results but no out-of-bounds
- * access.  No reference counterpart: the reference rejects packed sequences
+ * access.  `seqlen` must cover the longest document: a longer one is cut to
+ * its first `seqlen` tokens.  Token rows that no document covers (before
+ * cu[0], from cu[batch] on, the cut tail of a longer document) are written
+ * too: out rows 0 and m = -inf by ssa_varlen_fwd, dq / dk / dv rows 0 by
+ * ssa_varlen_bwd, so no output keeps stale memory.  No reference
+ * counterpart: the reference rejects packed sequences
  * (training/train/train_ssa_triton/SSA/ssa_triton_attention.py:154-156); the
  * layout is Megatron's PackedSeqParams (cu_seqlens_q, max_seqlen_q) as built
  * by training/finetune/nemo_patch/data/packed_sequence.py:116-244.

@@ -52,7 +52,7 @@ EXPORTED_SYMBOLS = (
     "ssa_cross_entropy",
 )
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class Tensor4(ctypes.Structure):

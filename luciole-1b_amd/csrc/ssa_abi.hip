@@ -43,50 +43,6 @@ Tensor4 to_t4(const ssa_tensor4& t) { return Tensor4{t.ptr, t.stride_b, t.stride
     if (st_ != SSA_OK) return st_;    \
   } while (0)
 
-int32_t fill_bwd(const ssa_bwd_args* a, ssa::BwdParams* p, bool preprocess_only) {
-  if (a == nullptr) return SSA_ERR_NULL_POINTER;
-  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
-  SSA_TRY(check_tensor(a->out, true));
-  SSA_TRY(check_tensor(a->dout, true));
-  if (a->delta == nullptr) return SSA_ERR_NULL_POINTER;
-  if (!preprocess_only) {
-    SSA_TRY(check_tensor(a->q, true));
-    SSA_TRY(check_tensor(a->k, true));
-    SSA_TRY(check_tensor(a->v, true));
-    SSA_TRY(check_tensor(a->dq, true));
-    SSA_TRY(check_tensor(a->dk, true));
-    SSA_TRY(check_tensor(a->dv, true));
-    if (a->m == nullptr || a->partials == nullptr || a->dn == nullptr || a->db == nullptr ||
-        a->ssa_n == nullptr || a->ssa_b == nullptr)
-      return SSA_ERR_NULL_POINTER;
-  }
-  p->q = to_t4(a->q);
-  p->k = to_t4(a->k);
-  p->v = to_t4(a->v);
-  p->o = to_t4(a->out);
-  p->dout = to_t4(a->dout);
-  p->dq = to_t4(a->dq);
-  p->dk = to_t4(a->dk);
-  p->dv = to_t4(a->dv);
-  p->m = a->m;
-  p->delta = a->delta;
-  p->partials = a->partials;
-  p->dn = a->dn;
-  p->db = a->db;
-  p->n_ptr = a->ssa_n;
-  p->b_ptr = a->ssa_b;
-  p->B = a->batch;
-  p->Hq = a->heads_q;
-  p->Hkv = a->heads_kv;
-  p->N = a->seqlen;
-  p->scale = a->softmax_scale;
-  p->cu_seqlens = nullptr;
-  p->T = 0;
-  if (!preprocess_only && a->ds_workspace != nullptr && !aligned16(a->ds_workspace)) return SSA_ERR_ALIGNMENT;
-  p->ds = preprocess_only ? nullptr : a->ds_workspace;
-  return SSA_OK;
-}
-
 int32_t fill_fwd(const ssa_fwd_args* a, ssa::FwdParams* p) {
   if (a == nullptr) return SSA_ERR_NULL_POINTER;
   SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
@@ -139,6 +95,66 @@ int64_t decode_ws_bytes(int32_t B, int32_t Hq, int32_t D, int32_t splits) {
 }
 
 }  // namespace
+
+namespace ssa {
+
+// Validation and parameters of the backward entry points.  with_workspaces =
+// false (ssa_bwd_noalloc) ignores delta, partials and ds_workspace: the
+// caller of that entry point supplies them from its own storage.
+int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces) {
+  if (a == nullptr) return SSA_ERR_NULL_POINTER;
+  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
+  SSA_TRY(check_tensor(a->out, true));
+  SSA_TRY(check_tensor(a->dout, true));
+  if (with_workspaces && a->delta == nullptr) return SSA_ERR_NULL_POINTER;
+  if (!preprocess_only) {
+    SSA_TRY(check_tensor(a->q, true));
+    SSA_TRY(check_tensor(a->k, true));
+    SSA_TRY(check_tensor(a->v, true));
+    SSA_TRY(check_tensor(a->dq, true));
+    SSA_TRY(check_tensor(a->dk, true));
+    SSA_TRY(check_tensor(a->dv, true));
+    if (a->m == nullptr || (with_workspaces && a->partials == nullptr) || a->dn == nullptr || a->db == nullptr ||
+        a->ssa_n == nullptr || a->ssa_b == nullptr)
+      return SSA_ERR_NULL_POINTER;
+  }
+  p->q = to_t4(a->q);
+  p->k = to_t4(a->k);
+  p->v = to_t4(a->v);
+  p->o = to_t4(a->out);
+  p->dout = to_t4(a->dout);
+  p->dq = to_t4(a->dq);
+  p->dk = to_t4(a->dk);
+  p->dv = to_t4(a->dv);
+  p->m = a->m;
+  p->delta = a->delta;
+  p->partials = a->partials;
+  p->dn = a->dn;
+  p->db = a->db;
+  p->n_ptr = a->ssa_n;
+  p->b_ptr = a->ssa_b;
+  p->B = a->batch;
+  p->Hq = a->heads_q;
+  p->Hkv = a->heads_kv;
+  p->N = a->seqlen;
+  p->scale = a->softmax_scale;
+  p->cu_seqlens = nullptr;
+  p->T = 0;
+  if (with_workspaces && !preprocess_only && a->ds_workspace != nullptr && !aligned16(a->ds_workspace))
+    return SSA_ERR_ALIGNMENT;
+  p->ds = (preprocess_only || !with_workspaces) ? nullptr : a->ds_workspace;
+  return SSA_OK;
+}
+
+// The whole backward on one stream: preprocess, dK/dV, dQ, reduction.
+int32_t run_bwd(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s) {
+  SSA_TRY(launch_status(launch_bwd_preprocess(p, dtype, D, s)));
+  SSA_TRY(launch_status(launch_bwd_dkdv(p, dtype, D, causal, s)));
+  SSA_TRY(launch_status(launch_bwd_dq(p, dtype, D, causal, s)));
+  return launch_status(launch_reduce_partials(p, s));
+}
+
+}  // namespace ssa
 
 extern "C" {
 
@@ -243,15 +259,27 @@ int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* va, void* stream) {
   SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
   p.cu_seqlens = va->cu_seqlens;
   p.T = va->total_tokens;
-  return launch_status(
-      ssa::launch_fwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SSA_TRY(launch_status(ssa::launch_fwd(p, a->dtype, a->head_dim, a->causal != 0, s)));
+  ssa::VarlenFill f{};
+  f.t[0] = p.o;
+  f.heads[0] = a->heads_q;
+  f.ntensors = 1;
+  f.m = a->m;
+  f.m_heads = a->heads_q;
+  f.cu = va->cu_seqlens;
+  f.B = a->batch;
+  f.T = va->total_tokens;
+  f.Nmax = a->seqlen;
+  f.D = a->head_dim;
+  return launch_status(ssa::launch_varlen_fill(f, s));
 }
 
 int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   if (va == nullptr) return SSA_ERR_NULL_POINTER;
   const ssa_bwd_args* a = &va->dense;
   ssa::BwdParams p{};
-  SSA_TRY(fill_bwd(a, &p, false));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
   SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
   p.cu_seqlens = va->cu_seqlens;
   p.T = va->total_tokens;
@@ -265,44 +293,52 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   SSA_TRY(launch_status(ssa::launch_bwd_preprocess(pre, a->dtype, a->head_dim, s)));
   SSA_TRY(launch_status(ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, causal, s)));
   SSA_TRY(launch_status(ssa::launch_bwd_dq(p, a->dtype, a->head_dim, causal, s)));
-  return launch_status(ssa::launch_reduce_partials(p, s));
+  SSA_TRY(launch_status(ssa::launch_reduce_partials(p, s)));
+  ssa::VarlenFill f{};
+  f.t[0] = p.dq;
+  f.t[1] = p.dk;
+  f.t[2] = p.dv;
+  f.heads[0] = a->heads_q;
+  f.heads[1] = f.heads[2] = a->heads_kv;
+  f.ntensors = 3;
+  f.cu = va->cu_seqlens;
+  f.B = a->batch;
+  f.T = va->total_tokens;
+  f.Nmax = a->seqlen;
+  f.D = a->head_dim;
+  return launch_status(ssa::launch_varlen_fill(f, s));
 }
 
 int32_t ssa_bwd_preprocess(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(fill_bwd(a, &p, true));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, true, true));
   return launch_status(ssa::launch_bwd_preprocess(p, a->dtype, a->head_dim, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_dkdv(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(fill_bwd(a, &p, false));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
   return launch_status(
       ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_dq(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(fill_bwd(a, &p, false));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
   return launch_status(
       ssa::launch_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_reduce(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(fill_bwd(a, &p, false));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
   return launch_status(ssa::launch_reduce_partials(p, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(fill_bwd(a, &p, false));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool causal = a->causal != 0;
-  SSA_TRY(launch_status(ssa::launch_bwd_preprocess(p, a->dtype, a->head_dim, s)));
-  SSA_TRY(launch_status(ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, causal, s)));
-  SSA_TRY(launch_status(ssa::launch_bwd_dq(p, a->dtype, a->head_dim, causal, s)));
-  return launch_status(ssa::launch_reduce_partials(p, s));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
+  return ssa::run_bwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -16,6 +16,32 @@ hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t stream);
 
+}  // namespace ssa
+
+struct ssa_bwd_args;  // include/ssa_mi355x.h
+
+namespace ssa {
+
+// Backward entry points (ssa_abi.hip): validation + parameters, and the four
+// launches of a whole backward in order.  with_workspaces = false leaves
+// delta, partials and ds unset for a caller that supplies them itself.
+int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces);
+int32_t run_bwd(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s);
+
+// Packed batches: write the token rows no document covers (ssa_varlen_fill.hip):
+// up to three [T, H, D] bf16/fp16 tensors (rows set to 0) and optionally an
+// [m_heads, T] fp32 normaliser (set to -inf).
+struct VarlenFill {
+  Tensor4 t[3];
+  int heads[3];
+  int ntensors;
+  float* m;
+  int m_heads;
+  const int* cu;
+  int B, T, Nmax, D;
+};
+hipError_t launch_varlen_fill(const VarlenFill& f, hipStream_t stream);
+
 // Decode key splits.  A split covers decode_split_keys() keys (a multiple of
 // 128); the default asks for about 256 workgroups (one per CU: a second
 // round of workgroups costs more than the longer splits save) but no split

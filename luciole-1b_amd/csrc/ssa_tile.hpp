@@ -69,9 +69,19 @@ struct LoadLane {
 // wait in front of later LDS transpose reads, which would drain the tile
 // prefetch; issued from assembly the loads are invisible to it, and the
 // kernels order them explicitly (wait_vm<N>() + barrier before a tile is
-// read).  M0 holds the LDS destination (wave-uniform); one wait state is
-// required between writing M0 and the load.  No builtin that uses M0 is
-// compiled into these kernels.
+// read).  M0 holds the LDS destination (wave-uniform).  It is an input operand
+// of each statement ("{m0}" constraint), so the compiler writes M0 itself and
+// knows it is live there.
+//
+// Wait states.  The compiler inserts the NOPs that hardware hazards need only
+// around instructions it can see: for an inline-assembly statement it checks
+// the registers the statement writes, not the ones it reads.  A vector-memory
+// instruction that reads an SGPR written by a VALU instruction (v_readfirstlane
+// of an offset, v_readlane reloading a spilled descriptor word) needs 5 wait
+// states in between, and one that reads M0 after an SALU write of M0 needs 1;
+// without them it can take the SGPR's previous value, i.e. a wrong address.
+// Every statement below that issues a vector-memory instruction with SGPR
+// operands therefore starts with s_nop 4 (5 wait states) itself.
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer descriptor: base address, stride 0, no bounds check in practice.
@@ -83,26 +93,26 @@ __device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
 
 // 16 bytes per lane from rsrc.base + voff + soff to LDS [m0 + 16 lane].
 __device__ __forceinline__ void dma_buffer16(uint32_t lds, const i32x4_t& rsrc, uint32_t voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory", "m0");
+               : "{m0}"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory");
 }
 
 // 16 bytes per lane from a per-lane global address to LDS [m0 + 16 lane].
 __device__ __forceinline__ void dma_global16(uint32_t lds, const void* src) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
                :
-               : "s"(lds), "v"(reinterpret_cast<uint64_t>(src))
-               : "memory", "m0");
+               : "{m0}"(lds), "v"(reinterpret_cast<uint64_t>(src))
+               : "memory");
 }
 
 // 4 bytes per lane from a per-lane global address to LDS [m0 + 4 lane].
 __device__ __forceinline__ void dma_global4(uint32_t lds, const void* src) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %1, off"
                :
-               : "s"(lds), "v"(reinterpret_cast<uint64_t>(src))
-               : "memory", "m0");
+               : "{m0}"(lds), "v"(reinterpret_cast<uint64_t>(src))
+               : "memory");
 }
 
 // 8 bytes to global memory at p + OFF bytes: exactly one vector-memory
@@ -117,7 +127,7 @@ __device__ __forceinline__ void store_b64(void* p, u32x2 v) {
 // 8 bytes to rs.base + voff + soff + OFF: one vector-memory instruction.
 template <int OFF>
 __device__ __forceinline__ void buffer_store_b64(const i32x4_t& rs, uint32_t voff, int soff, u32x2 v) {
-  asm volatile("buffer_store_dwordx2 %0, %1, %2, %3 offen offset:%4"
+  asm volatile("s_nop 4\n\tbuffer_store_dwordx2 %0, %1, %2, %3 offen offset:%4"
                :
                : "v"(v), "v"(voff), "s"(rs), "s"(soff), "i"(OFF)
                : "memory");

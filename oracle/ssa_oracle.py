@@ -144,6 +144,77 @@ def ssa_forward_backward(q, k, v, dout, scale, n, b, causal=True, out_for_delta=
     return {"out": out, "m": m, "dq": dq, "dk": dk, "dv": dv, "dn": dn, "db": db, "delta": delta}
 
 
+def ssa_forward_backward_chunked(q, k, v, dout, scale, n, b, causal=True, out_for_delta=None, chunk=512):
+    """``ssa_forward_backward`` evaluated one block of ``chunk`` query rows at a
+    time, so that no [N, N] matrix is built whole (a 16k x 16k float64 score
+    matrix alone is 2 GiB).  Every row's softmax, and so every quantity of the
+    forward and of dq, is a function of that row alone; dk, dv, dn and db are
+    sums over rows and are accumulated block by block.  Same arguments and
+    result keys as ``ssa_forward_backward`` (pinned against it in
+    tests/test_oracle.py).  The math is the dense function's:
+    ``check_ssa_triton_parity.py:169-237`` and ``ssa_triton_kernel.py:359-397``.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    do = np.asarray(dout, dtype=np.float64)
+    ofd = None if out_for_delta is None else np.asarray(out_for_delta, dtype=np.float64)
+    bsz, hq, nq, d = q.shape
+    hkv, nk = k.shape[1], k.shape[2]
+    if hq % hkv != 0:
+        raise ValueError(f"Hq={hq} must be divisible by Hkv={hkv}")
+    g = hq // hkv
+    res = {
+        "out": np.zeros((bsz, hq, nq, d)),
+        "m": np.full((bsz, hq, nq), -np.inf),
+        "delta": np.zeros((bsz, hq, nq)),
+        "dq": np.zeros((bsz, hq, nq, d)),
+        "dk": np.zeros((bsz, hkv, nk, d)),
+        "dv": np.zeros((bsz, hkv, nk, d)),
+        "dn": 0.0,
+        "db": 0.0,
+    }
+    for bi in range(bsz):
+        for h in range(hq):
+            kh, vh = k[bi, h // g], v[bi, h // g]
+            for a in range(0, nq, chunk):
+                e = min(a + chunk, nq)
+                ke = min(e, nk) if causal else nk  # keys any row of the block can see
+                if ke <= 0:
+                    continue
+                qc, doc = q[bi, h, a:e], do[bi, h, a:e]
+                s = scale * (qc @ kh[:ke].T)
+                if causal:  # key j visible to query i iff j <= i (top-left aligned)
+                    valid = np.arange(ke)[None, :] <= np.arange(a, e)[:, None]
+                else:
+                    valid = np.ones((e - a, ke), dtype=bool)
+                s0 = np.where(valid, s, 0.0)
+                lg = np.log1p(b * np.abs(s0))
+                sg = np.sign(s0)
+                t = np.where(valid, n * sg * lg, -np.inf)
+                tmax = np.max(t, axis=-1, keepdims=True)
+                tmax = np.where(np.isfinite(tmax), tmax, 0.0)
+                w = np.where(valid, np.exp(t - tmax), 0.0)
+                l = w.sum(axis=-1, keepdims=True)
+                p = np.where(l > 0, w / np.where(l > 0, l, 1.0), 0.0)
+                out = p @ vh[:ke]
+                res["out"][bi, h, a:e] = out
+                with np.errstate(divide="ignore"):
+                    res["m"][bi, h, a:e] = ((tmax + np.log(l)) / LN2)[:, 0]
+                oc = out if ofd is None else ofd[bi, h, a:e]
+                delta = np.sum(doc * oc, axis=-1)
+                res["delta"][bi, h, a:e] = delta
+                dp = doc @ vh[:ke].T
+                dt = p * (dp - delta[:, None])
+                ds = dt * (n * b / (1.0 + b * np.abs(s0)))
+                res["dq"][bi, h, a:e] = scale * (ds @ kh[:ke])
+                res["dk"][bi, h // g, :ke] += scale * (ds.T @ qc)
+                res["dv"][bi, h // g, :ke] += p.T @ doc
+                res["dn"] += float(np.sum(dt * sg * lg))
+                res["db"] += float(np.sum(dt * n * sg * np.abs(s0) / (1.0 + b * np.abs(s0))))
+    return res
+
+
 def ssa_varlen_forward_backward(q, k, v, dout, cu_seqlens, scale, n, b, causal=True, out_for_delta=None):
     """Packed-sequence SSA: q [T, Hq, D], k/v [T, Hkv, D], cu_seqlens int [ndocs+1].
 

@@ -350,3 +350,46 @@ def test_cross_entropy_validation():
         assert lib.ssa_cross_entropy(ctypes.byref(a), None) == status, field
     a = _lib.CrossEntropyArgs(FAKE, FAKE, None, FAKE, None, FAKE, 4, 64, 0, 1)  # backward needs scale
     assert lib.ssa_cross_entropy(ctypes.byref(a), None) == 1
+
+
+def test_hazard_scan_flags_short_waits():
+    """SSA/_hazards.py, the build's wait-state check, on hand-written sequences:
+    a VALU write of an SGPR needs 5 wait states before a vector-memory
+    instruction reads it (descriptor or offset), an SALU write of M0 one
+    before an LDS DMA; a label in between does not hide a fall-through path."""
+    from SSA import _hazards
+
+    def sites(body):
+        return _hazards.scan_asm("_Zk:\n" + "\n".join("\t" + ln for ln in body))
+
+    bad_off = ["v_readfirstlane_b32 s5, v1", "s_nop 0", "buffer_load_dwordx4 v2, s[8:11], s5 offen lds"]
+    assert [s[1:3] for s in sites(bad_off)] == [(1, 5)]
+    ok_off = ["v_readfirstlane_b32 s5, v1", "s_nop 4", "buffer_load_dwordx4 v2, s[8:11], s5 offen lds"]
+    assert sites(ok_off) == []
+    bad_rsrc = ["v_readlane_b32 s11, v180, 3", "s_add_i32 s4, s4, 1", ".LBB0_2:", "s_mov_b32 s6, 0",
+                "buffer_store_dwordx2 v[4:5], v2, s[8:11], s4 offen offset:8"]
+    assert [s[1:3] for s in sites(bad_rsrc)] == [(2, 5)]
+    bad_m0 = ["s_add_i32 m0, s3, 0x400", "global_load_lds_dwordx4 v[2:3], off"]
+    assert [s[1:3] for s in sites(bad_m0)] == [(0, 1)]
+    assert sites(["s_mov_b32 m0, s3", "s_nop 0", "global_load_lds_dwordx4 v[2:3], off"]) == []
+    # the form the tile loads had before: M0 written right before the load does
+    # not hide a VALU write of the descriptor two instructions back
+    both = ["v_readlane_b32 s11, v152, 20", "s_mov_b32 m0, s3", "s_nop 0",
+            "buffer_load_dwordx4 v2, s[8:11], s5 offen lds"]
+    assert [s[1:3] for s in sites(both)] == [(2, 5)]
+    # an SGPR the memory instruction does not read, and a VALU write far enough back
+    assert sites(["v_readfirstlane_b32 s7, v1", "buffer_load_dwordx4 v2, s[8:11], s5 offen lds"]) == []
+    far = ["v_readfirstlane_b32 s5, v1"] + ["v_add_f32_e32 v3, v3, v3"] * 5 + [
+        "buffer_load_dwordx4 v2, s[8:11], s5 offen lds"]
+    assert sites(far) == []
+
+
+def test_built_device_assembly_has_no_short_waits():
+    """The assembly the last build() checked (luciole-1b_amd/_build/*.gfx950.s),
+    re-scanned: no vector-memory instruction reads a register too soon."""
+    from SSA import _hazards
+
+    asms = sorted((ROOT / "luciole-1b_amd" / "_build").glob("*.gfx950.s"))
+    if not asms:
+        pytest.skip("no device assembly: run build() first")
+    assert _hazards.check_files(asms) == []

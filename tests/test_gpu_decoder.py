@@ -116,6 +116,74 @@ def test_decoder_cached_generation_equals_prefix_recompute(gpu):
     torch.cuda.synchronize()
 
 
+def test_decoder_full_size_train_steps(gpu):
+    """BASELINE.json configs[4] at its real size: ``SSADecoderConfig()`` (24
+    layers, hidden 2048, 16 x 128 heads, SwiGLU 5632, vocab 65536), micro-batch
+    4 x 4096 tokens, three ``train_step`` calls with fused AdamW (the layer
+    order of ssa_triton_layer_specs.py:96-127).  The first loss is
+    ln 65536 + init_std^2 * hidden / 2 (Gaussian logits at init), losses and every gradient are
+    finite, every layer's n moves, and one head of one layer's attention output
+    (captured at the op boundary during the first step) equals the fp64 oracle
+    of that head's own q / k / v, as the kernels' full-size tests check it."""
+    import math as _math
+
+    import numpy as np
+
+    from oracle import ssa_oracle as so
+    from parity_util import assert_parity, compare
+    from SSA.ssa_decoder import SSADecoder, SSADecoderConfig, train_step
+
+    cfg = SSADecoderConfig()
+    B, S = 4, cfg.seq_length
+    print(f"[gpu case] decoder full size: {cfg.num_layers} layers, hidden {cfg.hidden_size}, vocab "
+          f"{cfg.vocab_size}, {B} x {S} tokens", file=sys.stderr, flush=True)
+    torch.manual_seed(3)
+    model = SSADecoder(cfg).to(gpu)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device=gpu)
+    labels = torch.randint(0, cfg.vocab_size, (B, S), device=gpu)
+    layer_i, bi, h = 11, 2, 7
+    core = model.layers[layer_i].self_attention.core_attention
+    seen = {}
+
+    def hook(mod, args, out):
+        if "q" not in seen:
+            seen.update(q=args[0].detach().clone(), k=args[1].detach().clone(), v=args[2].detach().clone(),
+                        out=out.detach().clone())
+
+    handle = core.register_forward_hook(hook)
+    n0 = [l.self_attention.core_attention.ssa_n_raw.item() for l in model.layers]
+    losses = []
+    for step in range(3):
+        losses.append(train_step(model, opt, ids, labels).item())
+        bad = [n_ for n_, p_ in model.named_parameters() if p_.grad is not None and not torch.isfinite(p_.grad).all()]
+        assert not bad, f"step {step}: non-finite gradients in {bad[:5]}"
+        print(f"[gpu result] decoder full size step {step}: loss {losses[-1]:.4f}", file=sys.stderr, flush=True)
+    handle.remove()
+    torch.cuda.synchronize()
+    assert all(_math.isfinite(x) for x in losses), losses
+    # Gaussian logits at init (variance init_std^2 * hidden after the final
+    # RMSNorm): the expected cross-entropy is ln V + var / 2
+    expect0 = _math.log(cfg.vocab_size) + cfg.init_std ** 2 * cfg.hidden_size / 2
+    assert abs(losses[0] - expect0) < 0.1, (losses[0], expect0)
+    n1 = [l.self_attention.core_attention.ssa_n_raw.item() for l in model.layers]
+    assert all(a != b for a, b in zip(n0, n1)), "n did not move in every layer"
+
+    # one head of the captured attention call against the oracle
+    D = cfg.kv_channels
+    G = cfg.num_attention_heads // cfg.num_query_groups
+    q = seen["q"][:, bi, h].float().cpu().numpy().astype(np.float64)[None, None]          # [1, 1, S, D]
+    k = seen["k"][:, bi, h // G].float().cpu().numpy().astype(np.float64)[None, None]
+    v = seen["v"][:, bi, h // G].float().cpu().numpy().astype(np.float64)[None, None]
+    out = seen["out"].view(S, B, cfg.num_attention_heads, D)[:, bi, h][None, None]      # [1, 1, S, D]
+    ref = so.ssa_forward_backward_chunked(q, k, v, np.zeros_like(q), core.softmax_scale, n0[layer_i],
+                                          cfg.ssa_b, True)
+    res = compare({"out": out}, ref, names=("out",), scalars=())
+    print(f"[gpu result] decoder full size layer {layer_i + 1} head {h}: out max_abs "
+          f"{res['out']['max_abs']:.2e}", file=sys.stderr, flush=True)
+    assert_parity(res, "decoder full size attention head")
+
+
 @pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.bfloat16), (128, torch.float16)])
 def test_fused_rope_matches_torch(gpu, D, dtype):
     """ssa_rope (FusedRoPE) against the PyTorch rotate-half form in fp32, on a

@@ -89,3 +89,68 @@ def test_module_packed_sequences(gpu):
                                          np.ones((T, Hq, D)), cu.cpu().numpy(), 1.0 / math.sqrt(D), 1.5, 0.8, True)
     res = compare({"out": ctx.view(T, Hq, D), "dv": v.grad[:, 0]}, ref, names=("out", "dv"), scalars=())
     assert_parity(res, "module packed")
+
+
+@pytest.mark.parametrize("layer", [1, 6, 12])
+def test_module_query_key_layer_scaling(gpu, layer):
+    """apply_query_key_layer_scaling divides the softmax scale by the layer
+    number (ssa_triton_attention.py:91-97); the reference's module suite runs
+    layers 1, 6 and 12 (check_ssa_triton_parity.py:648-759, :1038)."""
+    from SSA.ssa_attention import SSAAttention
+
+    S, B, Hq, Hkv, D = 160, 2, 4, 2, 64
+    print(f"[gpu case] module layer scaling, layer {layer}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(100 + layer)
+    mk = lambda h: (torch.randn(S, B, h, D, generator=g) * 2.0).to(torch.bfloat16).to(gpu).requires_grad_()
+    q, k, v = mk(Hq), mk(Hkv), mk(Hkv)
+    mod = SSAAttention(Hq, Hkv, D, layer_number=layer, apply_query_key_layer_scaling=True).to(gpu)
+    scale = 1.0 / math.sqrt(D) / layer
+    assert mod.softmax_scale == pytest.approx(scale, rel=1e-12)
+    ctx = mod(q, k, v)
+    dctx = torch.randn(S, B, Hq * D, generator=g).to(torch.bfloat16).to(gpu)
+    ctx.backward(dctx)
+    torch.cuda.synchronize()
+    perm = lambda t: _np64(t).transpose(1, 2, 0, 3)
+    do = _np64(dctx.view(S, B, Hq, D)).transpose(1, 2, 0, 3)
+    got_out = ctx.view(S, B, Hq, D).permute(1, 2, 0, 3)
+    ref = so.ssa_forward_backward(perm(q), perm(k), perm(v), do, scale, 1.5, 0.8, True, out_for_delta=_np64(got_out))
+    res = compare({"out": got_out, "dq": q.grad.permute(1, 2, 0, 3), "dk": k.grad.permute(1, 2, 0, 3),
+                   "dv": v.grad.permute(1, 2, 0, 3)}, ref, scalars=())
+    assert_parity(res, f"module layer {layer}")
+    assert abs(mod.ssa_n_raw.grad.item() - ref["dn"]) <= 2e-3 + 2e-2 * abs(ref["dn"])
+    if layer > 1:  # the scale really changed the result
+        ref1 = so.ssa_forward(perm(q), perm(k), perm(v), 1.0 / math.sqrt(D), 1.5, 0.8, True)[0]
+        assert np.abs(ref1 - ref["out"]).max() > 0.1
+
+
+def test_module_output_dropout(gpu):
+    """Dropout is applied to the attention output after the op, never inside
+    it (ssa_triton_attention.py:187-193; SSAFlashAttnFunc ignores dropout_p):
+    in training every output element is either 0 or the undropped value /
+    (1 - p), about a fraction p are 0, and the gradient passes through the same
+    mask; in eval mode the output is the undropped one."""
+    from SSA.ssa_attention import SSAAttention
+
+    S, B, H, D, p = 128, 2, 4, 64, 0.25
+    print("[gpu case] module output dropout", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(5)
+    mk = lambda: (torch.randn(S, B, H, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu).requires_grad_()
+    q, k, v = mk(), mk(), mk()
+    ref_mod = SSAAttention(H, H, D, attention_dropout=0.0).to(gpu)
+    mod = SSAAttention(H, H, D, attention_dropout=p).to(gpu)
+    base = ref_mod(q, k, v).detach().float()
+    torch.manual_seed(0)
+    ctx = mod(q, k, v)
+    out = ctx.detach().float()
+    kept = out != 0
+    frac_dropped = 1.0 - kept.float().mean().item()
+    assert abs(frac_dropped - p) < 0.02, frac_dropped
+    scaled = (base / (1.0 - p)).to(torch.bfloat16).float()
+    assert torch.allclose(out[kept], scaled[kept], rtol=1e-2, atol=1e-3)
+    ctx.float().sum().backward()
+    gv = v.grad.detach().float()
+    assert torch.isfinite(gv).all() and gv.abs().sum() > 0
+    mod.eval()
+    with torch.no_grad():
+        ev = mod(q, k, v).float()
+    assert torch.equal(ev, base)

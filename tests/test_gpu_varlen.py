@@ -160,3 +160,30 @@ def test_varlen_malformed_table_is_clamped(gpu, ds):
     _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, 100, True, oracle_cu=[0, 40, 100], ds=ds)
     assert merr < 1e-2
     assert_parity(res, "clamped table")
+
+
+@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
+def test_varlen_uncovered_rows_are_written(gpu, ds):
+    """Tokens in no document -- after cu[-1] < T, and the tail of a document
+    longer than max_seqlen (cut to its first max_seqlen tokens) -- come back as
+    out = 0, m = -inf and dq = dk = dv = 0, never as stale memory: the caching
+    allocator is first filled with NaN blocks of the output sizes, which the
+    outputs then reuse."""
+    lens_cover, T, max_seqlen = (37, 83), 200, 60   # covered: [0, 37), [37, 97); tokens 97..199 are not
+    label = f"varlen uncovered rows ds={int(ds)}"
+    print(f"[gpu case] {label}", file=sys.stderr, flush=True)
+    Hq, Hkv, D = 4, 2, 64
+    q, k, v, do, _ = _inputs((T,), Hq, Hkv, D, torch.bfloat16, gpu)
+    poison = [torch.full((T, h, D), float("nan"), device=gpu, dtype=torch.bfloat16) for h in (Hq, Hq, Hkv, Hkv)]
+    poison.append(torch.full((Hq, T), float("nan"), device=gpu))
+    del poison
+    cu = torch.tensor([0, 37, 37 + 83], dtype=torch.int32)
+    out, m, (dq, dk, dv, dn, db), res, res_k, merr = _run(gpu, q, k, v, do, cu, max_seqlen, True,
+                                                          oracle_cu=[0, 37, 37 + max_seqlen], ds=ds)
+    for name, t in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert not torch.isnan(t).any(), f"{label}: {name} has NaN (stale rows)"
+        assert (t[97:] == 0).all(), f"{label}: {name} rows 97.. not zero"
+    assert torch.isneginf(m[:, 97:]).all(), f"{label}: m of uncovered rows"
+    assert merr < 1e-2
+    assert_parity(res, label)
+    assert_parity(res_k, label + " [kernel-level]")

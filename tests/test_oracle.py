@@ -306,3 +306,25 @@ def test_decode_is_last_row_of_causal_forward():
     out, m = so.ssa_decode(q_dec, kc, vc, [0, 0, 5, -3], 0.4, 1.5, 0.8)
     assert np.all(out[[0, 1, 3]] == 0.0) and np.all(np.isneginf(m[[0, 1, 3]]))
     assert np.all(np.isfinite(m[2]))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("chunk", [1, 7, 16, 64])
+def test_chunked_equals_dense(causal, chunk):
+    """The row-block evaluation (used at S = 16384, where the dense oracle's
+    N x N matrices do not fit) against the pinned dense oracle: same outputs
+    to rounding, for chunks that divide N, that do not, of one row and of the
+    whole sequence; with GQA, ragged N, the kernel-level out_for_delta, and
+    n values of both signs."""
+    rng = np.random.default_rng(21)
+    for (B, Hq, Hkv, N, D), n_val in (((2, 4, 2, 37, 8), 1.5), ((1, 3, 1, 64, 16), -3.484375)):
+        q, k, v, do = (_rand(rng, B, Hq, N, D), _rand(rng, B, Hkv, N, D), _rand(rng, B, Hkv, N, D),
+                       _rand(rng, B, Hq, N, D))
+        ofd = _rand(rng, B, Hq, N, D)
+        for out_for_delta in (None, ofd):
+            r = so.ssa_forward_backward(q, k, v, do, 0.3, n_val, 0.8, causal, out_for_delta)
+            rc = so.ssa_forward_backward_chunked(q, k, v, do, 0.3, n_val, 0.8, causal, out_for_delta, chunk=chunk)
+            for name in ("out", "m", "delta", "dq", "dk", "dv"):
+                np.testing.assert_allclose(rc[name], r[name], rtol=1e-11, atol=1e-12, err_msg=name)
+            for name in ("dn", "db"):
+                assert abs(rc[name] - r[name]) <= 1e-11 * max(1.0, abs(r[name])), name
