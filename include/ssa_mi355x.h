@@ -12,7 +12,8 @@
  *  - Every entry point validates its arguments on the host and returns a
  *    status (SSA_OK = 0) before any launch; nothing is launched on error.
  *  - The library never allocates or frees device memory.  Outputs and
- *    workspaces are passed in by the caller.
+ *    workspaces are passed in by the caller (ssa_bwd_noalloc instead uses a
+ *    fixed-size static device array of the library's code object).
  *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
  *    default stream).  No entry point synchronises the device or reads device
  *    memory on the host (n and b are read by the kernels through pointers).
@@ -46,7 +47,9 @@ enum {
                               /* stride negative or not a multiple of 8, or the   */
                               /* row stride >= 2^24 elements                      */
   SSA_ERR_LAUNCH = 6,         /* the HIP runtime rejected a kernel launch         */
-  SSA_ERR_CU_SEQLENS = 7      /* varlen: bad document table                       */
+  SSA_ERR_CU_SEQLENS = 7,     /* varlen: bad document table                       */
+  SSA_ERR_SCRATCH = 8         /* ssa_bwd_noalloc: the problem's Delta + partials  */
+                              /* exceed SSA_NOALLOC_SCRATCH_BYTES                 */
 };
 
 /* Element types of q/k/v/out/dout/dq/dk/dv. */
@@ -160,6 +163,24 @@ int32_t ssa_bwd_preprocess(const ssa_bwd_args* args, void* stream);
 int32_t ssa_bwd_dkdv(const ssa_bwd_args* args, void* stream);
 int32_t ssa_bwd_dq(const ssa_bwd_args* args, void* stream);
 int32_t ssa_bwd_reduce(const ssa_bwd_args* args, void* stream);
+
+/*
+ * ssa_bwd for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments and results as ssa_bwd, but
+ * args->delta, args->partials and args->ds_workspace are ignored: Delta and
+ * the dn/db partials live in a static device array of
+ * SSA_NOALLOC_SCRATCH_BYTES bytes that the library holds on every device it
+ * runs on until the process ends, and dq recomputes the scores (no dS'
+ * workspace).  Needs round256(4 * batch * heads_q * seqlen) +
+ * 8 * batch * heads_kv * ceil(seqlen / 128) bytes of it (B=4, H=16, S=4096:
+ * about 1 MiB); larger problems return SSA_ERR_SCRATCH with nothing
+ * launched.  Calls no allocating routine.  Every call on a device shares that
+ * device's array: calls in flight at the same time on one device (on
+ * different streams) race; calls in stream order do not.
+ */
+#define SSA_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int32_t ssa_bwd_noalloc(const ssa_bwd_args* args, void* stream);
 
 /*
  * Packed (varlen) sequences.  q/k/v/out (and dout/dq/dk/dv) are token streams

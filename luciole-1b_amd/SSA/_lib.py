@@ -22,6 +22,7 @@ SSA_ERR_DTYPE = 4
 SSA_ERR_ALIGNMENT = 5
 SSA_ERR_LAUNCH = 6
 SSA_ERR_CU_SEQLENS = 7
+SSA_ERR_SCRATCH = 8
 
 SSA_DTYPE_BF16 = 0
 SSA_DTYPE_FP16 = 1
@@ -38,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "ssa_bwd_dkdv",
     "ssa_bwd_dq",
     "ssa_bwd_reduce",
+    "ssa_bwd_noalloc",
     "ssa_varlen_fwd",
     "ssa_varlen_bwd",
     "ssa_varlen_bwd_ds_workspace_bytes",
@@ -242,7 +244,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssa_varlen_bwd_ds_workspace_bytes.restype = ctypes.c_int64
     lib.ssa_varlen_bwd_ds_workspace_bytes.argtypes = [ctypes.c_int32] * 5
     for name, argt in (("ssa_fwd", FwdArgs), ("ssa_bwd", BwdArgs), ("ssa_bwd_preprocess", BwdArgs),
-                       ("ssa_bwd_dkdv", BwdArgs), ("ssa_bwd_dq", BwdArgs), ("ssa_bwd_reduce", BwdArgs)):
+                       ("ssa_bwd_dkdv", BwdArgs), ("ssa_bwd_dq", BwdArgs), ("ssa_bwd_reduce", BwdArgs),
+                       ("ssa_bwd_noalloc", BwdArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int32
         fn.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
@@ -292,6 +295,7 @@ def check(status: int, what: str) -> None:
     if status == SSA_OK:
         return
     msg = f"{what}: {status_text(status)} (status {status})"
-    if status in (SSA_ERR_SHAPE, SSA_ERR_HEAD_DIM, SSA_ERR_DTYPE, SSA_ERR_ALIGNMENT, SSA_ERR_CU_SEQLENS):
+    if status in (SSA_ERR_SHAPE, SSA_ERR_HEAD_DIM, SSA_ERR_DTYPE, SSA_ERR_ALIGNMENT, SSA_ERR_CU_SEQLENS,
+                  SSA_ERR_SCRATCH):
         raise ValueError(msg)
     raise RuntimeError(msg)

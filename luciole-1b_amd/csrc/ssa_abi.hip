@@ -174,6 +174,9 @@ const char* ssa_status_string(int32_t status) {
     case SSA_ERR_CU_SEQLENS:
       return "invalid packed-sequence arguments (total_tokens, documents and max_seqlen must be > 0, "
              "max_seqlen <= total_tokens)";
+    case SSA_ERR_SCRATCH:
+      return "problem too large for the static scratch of ssa_bwd_noalloc (Delta plus the dn/db partials "
+             "must fit SSA_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }

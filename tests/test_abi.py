@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_status_strings():
-    for code in range(8):
+    for code in range(9):
         assert _lib.status_text(code)
     assert _lib.status_text(99) == "unknown status"
 
@@ -350,6 +350,41 @@ def test_cross_entropy_validation():
         assert lib.ssa_cross_entropy(ctypes.byref(a), None) == status, field
     a = _lib.CrossEntropyArgs(FAKE, FAKE, None, FAKE, None, FAKE, 4, 64, 0, 1)  # backward needs scale
     assert lib.ssa_cross_entropy(ctypes.byref(a), None) == 1
+
+
+@pytest.mark.parametrize(
+    "field,value,status",
+    [
+        ("heads_kv", 5, _lib.SSA_ERR_SHAPE),
+        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),
+        ("dtype", 2, _lib.SSA_ERR_DTYPE),
+        ("dn", None, _lib.SSA_ERR_NULL_POINTER),
+        ("m", None, _lib.SSA_ERR_NULL_POINTER),
+        ("dq", _lib.Tensor4(FAKE, 4, 0, 128), _lib.SSA_ERR_ALIGNMENT),
+    ],
+)
+def test_bwd_noalloc_validation(field, value, status):
+    a = _bwd_args(**{field: value})
+    assert _lib.lib().ssa_bwd_noalloc(ctypes.byref(a), None) == status
+
+
+def test_bwd_noalloc_rejects_problems_beyond_its_scratch():
+    """Delta (4 B per query row, rounded to 256 B) plus the partials (8 B per
+    128-key block and kv-head) must fit the 16 MiB static scratch; larger
+    problems are refused on the host, before any device call (this runs
+    without a GPU), and the caller's own workspace fields are never required."""
+    lim = 16 << 20
+    a = _bwd_args(delta=None, partials=None, ds_workspace=None)
+    assert _lib.lib().ssa_bwd_noalloc(None, None) == _lib.SSA_ERR_NULL_POINTER
+    # B * Hq * N * 4 bytes of Delta alone above the limit
+    a.batch, a.heads_q, a.heads_kv, a.seqlen = 64, 16, 16, 4097
+    assert 64 * 16 * 4097 * 4 > lim
+    assert _lib.lib().ssa_bwd_noalloc(ctypes.byref(a), None) == _lib.SSA_ERR_SCRATCH
+    # just above: Delta exactly 16 MiB leaves no room for the partials
+    a.batch, a.heads_q, a.heads_kv, a.seqlen = 64, 16, 16, 4096
+    assert 64 * 16 * 4096 * 4 == lim
+    assert _lib.lib().ssa_bwd_noalloc(ctypes.byref(a), None) == _lib.SSA_ERR_SCRATCH
+    assert "scratch" in _lib.status_text(_lib.SSA_ERR_SCRATCH)
 
 
 def test_hazard_scan_flags_short_waits():
