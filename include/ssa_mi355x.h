@@ -113,8 +113,9 @@ const char* ssa_status_string(int32_t status);
 int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen);
 
 /*
- * Bytes of the optional dS' workspace of ssa_bwd: dS' = dP (.) P / (1 + b|s|)
- * in the input dtype, per (batch, q-head) the 32-query x 16-key tiles of the
+ * Bytes of the optional dS' workspace of ssa_bwd: -dS' = P (.) (Delta - dP) /
+ * (1 + b|s|) in the input dtype (its contents are private to the dk/dv and dq
+ * launches of one backward), per (batch, q-head) the 32-query x 16-key tiles of the
  * causal triangle (all tiles without the mask), 2 * N^2 bytes + O(N) per head
  * causal, 4 * N^2 without.  With it, dk/dv writes dS' and dq becomes one
  * streaming product dS' K instead of a recompute of the scores (the

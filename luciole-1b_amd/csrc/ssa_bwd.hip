@@ -63,6 +63,13 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_kernel(BwdParams p) {
 // the S and dP products read row-wise.  K and V stay in registers, dK and dV
 // accumulate in AGPRs.
 //
+// Sign convention: the V fragments are held negated and the dP product starts
+// from Delta instead of zero, so its accumulator is Delta - dP = -(dP - Delta)
+// with no vector instruction per element; every per-pair quantity derived
+// from it (dT, dS', the dn / db terms) is therefore the negated one, and the
+// sign is restored where those sums leave the kernel (the dK scale, the dn / db
+// partials, and the dS' workspace, which holds -dS' for the dQ pass).
+//
 // Software pipeline, one slot per sub-tile: slot j issues the MFMAs of
 // dV/dK for sub-tile j - 1 and of S/dP for sub-tile j + 1, and the vector
 // work of sub-tile j (SSA transform, P, dS', dn/db sums).  The two streams are
@@ -101,6 +108,50 @@ struct StepWalk {
   }
   __device__ __forceinline__ int sub_unmasked(int nlo) const { return nlo + j; }
 };
+
+// Store one wave's 32 keys x D block of dK or dV: the lane holds d = 32 db +
+// l32 of key rows k0w + crow(r, hh).  The block goes through the wave's own
+// LDS tile `tile` ([d][key], 72-byte rows) so that every lane stores 8 bytes
+// (4 consecutive d of one key) per instruction.  Write: lane (l32, hh), keys
+// 8 a + 4 hh .. + 3 of row d.  Transposed read t: in 16-lane group g, lane
+// 4 e + q supplies row 8 t + 4 (g >> 1) + e, keys 16 (g & 1) + 4 q .. + 3, so
+// lane 16 g + i receives key 16 (g & 1) + i, d = 8 t + 4 (g >> 1) + (0..3).
+// `rows` is row 0 of the (sequence, kv-head) slice, `ss` its row stride.
+template <typename T, int D>
+__device__ __forceinline__ void store_key_block(const f32x16* acc, float scale, T* rows, int64_t ss, int k0w, int N,
+                                                uint32_t tile, int lane) {
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  constexpr int RS = 72, ND32 = D / 32;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const uint32_t wr0 = tile + l32 * RS + hh * 8;
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const uint32_t rd0 = tile + (4 * (g16 >> 1) + (s16 >> 2)) * RS + (16 * (g16 & 1) + 4 * (s16 & 3)) * 2;
+  const int okey = k0w + 16 * (g16 & 1) + s16;
+  const int od0 = 4 * (g16 >> 1);
+#pragma unroll
+  for (int db = 0; db < ND32; ++db) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      v4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[db][4 * a + e] * scale);
+      *(__attribute__((address_space(3))) v4*)(uintptr_t)(wr0 + db * 32 * RS + a * 16) = w;
+    }
+  }
+  T* row = rows + static_cast<int64_t>(min(okey, N - 1)) * ss + od0;
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i) {
+    const v4 r = __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                            (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(rd0 + i * 8 * RS)));
+    if (okey < N) *reinterpret_cast<v4*>(row + 8 * i) = r;
+  }
+}
+// Byte size of one wave's tile for store_key_block.
+template <int D>
+constexpr int key_block_tile_bytes() {
+  return D * 72;
+}
 
 // OFF32: every Q / dO row a workgroup reads lies below 2 GiB of its base
 // (q-head hk G of the sequence), and so does its dS' range (checked on the
@@ -227,7 +278,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
   for (int ds = 0; ds < ND16; ++ds) {
     kf[ds] = key < N ? load16<v8>(kg + key * p.k.ss + ds * 16 + 8 * hh) : zero8<v8>();
-    vf[ds] = key < N ? load16<v8>(vg + key * p.v.ss + ds * 16 + 8 * hh) : zero8<v8>();
+    // negated V: flip the sign bit of every 16-bit element
+    vf[ds] = key < N ? __builtin_bit_cast(v8, __builtin_bit_cast(u32x4, load16<v8>(vg + key * p.v.ss + ds * 16 + 8 * hh)) ^
+                                                  u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u})
+                     : zero8<v8>();
   }
 
   f32x16 dk[ND32], dv[ND32];
@@ -253,10 +307,22 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   };
 
   // ---- generic pieces (masked steps, pipeline fill and drain) ----
+  // Delta of the 16 query rows crow(r, hh) of sub-tile st, as a dP accumulator
+  auto delta_rows = [&](int st) {
+    const uint32_t ml = bufof(st) + 2 * TILE + 128;
+    f32x4_t d4[4];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) d4[g4] = lds_read_f4(ml + (8 * g4 + 4 * hh) * 4);
+    f32x16 r;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r[e] = d4[e >> 2][e & 3];
+    return r;
+  };
+  // S and Delta - dP of sub-tile st
   auto sdp = [&](int st, f32x16& s_out, f32x16& d_out) {
     const RowBase<D> rq = at_tile(rb, bufof(st)), rd = at_tile(rb, bufof(st) + TILE);
     s_out = f32x16{};
-    d_out = f32x16{};
+    d_out = delta_rows(st);
 #pragma unroll
     for (int ds = 0; ds < ND16; ++ds) {
       s_out = mfma32(tile_read_row<D, v8>(rq, 0, ds), kf[ds], s_out);
@@ -287,7 +353,6 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x4_t mv = lds_read_f4(ml + (8 * j + 4 * hh) * 4);
-      const f32x4_t dv4 = lds_read_f4(ml + 128 + (8 * j + 4 * hh) * 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * j + e;
@@ -300,12 +365,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
           const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
           pv = valid ? pv : 0.f;
         }
-        const float dt = pv * (dc[r] - dv4[e]);
-        const float dsp = dt * fast_rcp(u1);
-        tdn = fmaf(dt, sl, tdn);
-        tdb = fmaf(dsp, x, tdb);
+        const float ndt = pv * dc[r];  // -dT (dc = Delta - dP)
+        const float nds = ndt * fast_rcp(u1);
+        tdn = fmaf(ndt, sl, tdn);
+        tdb = fmaf(nds, x, tdb);
         pa2[r >> 3][r & 7] = static_cast<T>(pv);
-        sa2[r >> 3][r & 7] = static_cast<T>(dsp);
+        sa2[r >> 3][r & 7] = static_cast<T>(nds);
       }
     }
     kahan(tdn, tdb);
@@ -319,22 +384,23 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       sa[ks] = sa2[ks];
     }
   };
-  // dS' of sub-tile st to the workspace (DS): this wave's 32 keys are key
+  // -dS' of sub-tile st to the workspace (DS): this wave's 32 keys are key
   // tiles kj0 = k0w / 16 and kj0 + 1 of query tile q0 / 32 (both inside the
   // causal triangle when the sub-tile is not skipped).  Lane (l32, hh) holds
   // key l32 and, in sa2[ks], queries 16 ks + 4 hh + (0..3) (elements 0..3) and
   // 16 ks + 8 + 4 hh + (0..3) (elements 4..7): in the tile format (lane
   // 16 g + kl: key kl, queries 16 t + 4 g + (0..3) at elements 4 t ..) these
-  // are four 8-byte pieces, g = hh or 2 + hh, t = ks.
+  // are four 8-byte pieces, g = hh or 2 + hh, t = ks; the two of one g are
+  // adjacent, so the lane writes two 16-byte pieces.
   // workspace tile (32 x 16) of q-head hk * G + g, query tile qi, key tile k0w / 16:
   // head_tile(b, hk G) + g tiles_per_head + row_offset(qi) + k0w / 16, 512 elements each
   const int64_t ds_tph = ds_tiles_per_head(N, CAUSAL);
   T* const ds_head0 =
       static_cast<T*>(p.ds) + (ds_head_tile(sv.packed, sv.tok0, b, hk * G, p.Hq, N, p.N, CAUSAL) + (k0w >> 4)) * 512;
   const uint32_t ds_lane = (l32 >> 4) * 512 + (l32 & 15) * 8;
-  // Exactly four vector-memory instructions (the fast slot's load wait
+  // Exactly two vector-memory instructions (the fast slot's load wait
   // counts them): piece (g, t) at byte 256 g + 8 t of the lane's slot, so
-  // from 256 hh: +0, +8 (g = hh), +512, +520 (g = 2 + hh).
+  // from 256 hh: +0 (g = hh, t = 0 and 1), +512 (g = 2 + hh).
   const i32x4_t ds_rs = raw_rsrc(ds_head0);
   const uint32_t ds_voff = (ds_lane + (16 * hh) * 8) * 2;
   const int ds_tph1k = static_cast<int>(ds_tph * 1024);
@@ -345,16 +411,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       const int qi = q0 >> 5;
       const int soff = __builtin_amdgcn_readfirstlane(w.g * ds_tph1k +
                                                       (CAUSAL ? qi * (qi + 1) : qi * 2 * ((N + 31) >> 5)) * 1024);
-      buffer_store_b64<0>(ds_rs, ds_voff, soff, u32x2{s0[0], s0[1]});
-      buffer_store_b64<8>(ds_rs, ds_voff, soff, u32x2{s1[0], s1[1]});
-      buffer_store_b64<512>(ds_rs, ds_voff, soff, u32x2{s0[2], s0[3]});
-      buffer_store_b64<520>(ds_rs, ds_voff, soff, u32x2{s1[2], s1[3]});
+      buffer_store_b128_nt<0>(ds_rs, ds_voff, soff, u32x4{s0[0], s0[1], s1[0], s1[1]});
+      buffer_store_b128_nt<512>(ds_rs, ds_voff, soff, u32x4{s0[2], s0[3], s1[2], s1[3]});
     } else {
       T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane + (16 * hh) * 8;
-      store_b64<0>(dst, u32x2{s0[0], s0[1]});
-      store_b64<8>(dst, u32x2{s1[0], s1[1]});
-      store_b64<512>(dst, u32x2{s0[2], s0[3]});
-      store_b64<520>(dst, u32x2{s1[2], s1[3]});
+      store_b128_nt<0>(dst, u32x4{s0[0], s0[1], s1[0], s1[1]});
+      store_b128_nt<512>(dst, u32x4{s0[2], s0[3], s1[2], s1[3]});
     }
   };
   auto slot_generic = [&](int j) {
@@ -390,7 +452,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     constexpr int NG = 4 * ND32 + 2 * ND16;  // MFMAs per slot
     constexpr int STRIDE = 32 / NG;           // ticks per MFMA
     // Sub-tile j + 1 (issued in slot j - 1).  The vector-memory counter also
-    // counts stores, in issue order: slot j - 1 ended with its four dS' stores
+    // counts stores, in issue order: slot j - 1 ended with its two dS' stores
     // (an unmasked slot always stores; a masked one unless its step was
     // skipped), which may stay in flight.
     if constexpr (!DS) {
@@ -399,9 +461,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       if (skipped(j - 1))
         wait_vm<0>();
       else
-        wait_vm<4>();
+        wait_vm<2>();
     } else {
-      wait_vm<4>();
+      wait_vm<2>();
     }
     __builtin_amdgcn_s_barrier();
     issue(j + 2, wi, std::integral_constant<bool, !MASKED>{});
@@ -414,12 +476,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const TrBase<D> tq = at_tile(tb, bufof(j - 1)), td = at_tile(tb, bufof(j - 1) + TILE);
     const RowBase<D> rq = at_tile(rb, bufof(j + 1)), rd = at_tile(rb, bufof(j + 1) + TILE);
     const uint32_t ml = bufof(j) + 2 * TILE;
-    f32x4_t mq[4], dq4[4];
+    f32x4_t mq[4];
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      mq[g4] = lds_read_f4(ml + (8 * g4 + 4 * hh) * 4);
-      dq4[g4] = lds_read_f4(ml + 128 + (8 * g4 + 4 * hh) * 4);
-    }
+    for (int g4 = 0; g4 < 4; ++g4) mq[g4] = lds_read_f4(ml + (8 * g4 + 4 * hh) * 4);
+    const f32x16 dnext = delta_rows(j + 1);  // accumulator start of dP of sub-tile j + 1
     v8 ops[3];
     // MFMA g: g < 4 ND32 -> dV (even) / dK (odd) of sub-tile j - 1, pair (ks, db);
     // else S (even) / dP (odd) of sub-tile j + 1, contraction slice ds.
@@ -449,15 +509,15 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         if constexpr (h % 2 == 0)
           sn = mfma32(ops[Gi % 3], kf[ds], ds == 0 ? f32x16{} : sn);
         else
-          dn2 = mfma32(ops[Gi % 3], vf[ds], ds == 0 ? f32x16{} : dn2);
+          dn2 = mfma32(ops[Gi % 3], vf[ds], ds == 0 ? dnext : dn2);
       }
     };
-    // element pipeline over the 16 entries of S_j / dP_j
+    // element pipeline over the 16 entries of S_j / (Delta - dP)_j
     //   A: u = 1 + c|x|, L = log2 u, 1/u
-    //   B: sL = copysign(L, x), p = exp2(n sL - M), dd = dP - Delta
-    //   C1: dT = p dd, dS' = dT / u      C2: dn, db sums, bf16 operands
+    //   B: sL = copysign(L, x), p = exp2(n sL - M)
+    //   C1: -dT = p (Delta - dP), -dS' = -dT / u      C2: dn, db sums, bf16 operands
     // tick 2e: A(e + 2), C1(e); tick 2e + 1: B(e + 1), C2(e)
-    float Lv[16], rv[16], slv[16], pv[16], ddv[16], dtv[16], dsv[16];
+    float Lv[16], rv[16], slv[16], pv[16], dtv[16], dsv[16];
     float tdn = 0.f, tdb = 0.f;
     auto A = [&](int e) {
       const float x = sc[e];
@@ -476,12 +536,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         const bool valid = qi < N && key < N && (!CAUSAL || key <= qi);
         pv[e] = valid ? pv[e] : 0.f;
       }
-      ddv[e] = dc[e] - dq4[e >> 2][e & 3];
       pin(pv[e]);
-      pin(ddv[e]);
     };
     auto C1 = [&](int e) {
-      dtv[e] = pv[e] * ddv[e];
+      dtv[e] = pv[e] * dc[e];
       dsv[e] = dtv[e] * rv[e];
       pin(dtv[e]);
       pin(dsv[e]);
@@ -549,44 +607,15 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   for (; j + 1 < nsteps; ++j) slot_fast(j, std::false_type{});
   for (; j <= nsteps; ++j) slot_generic(j);
 
-  // Store dK (scaled by scale * n * b) and dV.  The lane holds d = 32 db + l32
-  // of key rows crow(r, hh); each wave turns its 32 keys x D through its own
-  // LDS tile, [d][key] with 72-byte rows, so that every lane stores 8 bytes
-  // (4 consecutive d of one key) per instruction.  Write: lane (l32, hh), keys
-  // 8 a + 4 hh .. + 3 of row d.  Transposed read t: in 16-lane group g, lane
-  // 4 e + q supplies row 8 t + 4 (g >> 1) + e, keys 16 (g & 1) + 4 q .. + 3, so
-  // lane 16 g + i receives key 16 (g & 1) + i, d = 8 t + 4 (g >> 1) + (0..3).
+  // Store dK (scaled by scale * n * b; the accumulator holds -dK_raw) and dV.
   __syncthreads();  // every wave is done with the sub-tile ring (no loads in flight)
-  constexpr int RS = 72;
-  const uint32_t tile = lds0 + wave * (D * RS);
-  const uint32_t wr0 = tile + l32 * RS + hh * 8;
-  const int g16 = lane >> 4, s16 = lane & 15;
-  const uint32_t rd0 = tile + (4 * (g16 >> 1) + (s16 >> 2)) * RS + (16 * (g16 & 1) + 4 * (s16 & 3)) * 2;
-  const int okey = k0w + 16 * (g16 & 1) + s16;
-  const int od0 = 4 * (g16 >> 1);
-  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-  auto put = [&](const f32x16* acc, float scale, const Tensor4& t) {
-#pragma unroll
-    for (int db = 0; db < ND32; ++db) {
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        v4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[db][4 * a + e] * scale);
-        *(__attribute__((address_space(3))) v4*)(uintptr_t)(wr0 + db * 32 * RS + a * 16) = w;
-      }
-    }
-    T* row = static_cast<T*>(const_cast<void*>(t.ptr)) + sv.off(t, b) + hk * t.sh + min(okey, N - 1) * t.ss + od0;
-#pragma unroll
-    for (int i = 0; i < D / 8; ++i) {
-      const v4 r = __builtin_bit_cast(
-          v4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                  (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)(rd0 + i * 8 * RS)));
-      if (okey < N) *reinterpret_cast<v4*>(row + 8 * i) = r;
-    }
-  };
-  put(dk, p.scale * n * *p.b_ptr, p.dk);
-  put(dv, 1.f, p.dv);
+  {
+    const uint32_t tile = lds0 + wave * key_block_tile_bytes<D>();
+    T* dkr = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;
+    T* dvr = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh;
+    store_key_block<T, D>(dk, -(p.scale * n * *p.b_ptr), dkr, p.dk.ss, k0w, N, tile, lane);
+    store_key_block<T, D>(dv, 1.f, dvr, p.dv.ss, k0w, N, tile, lane);
+  }
 
   // dn / db partial of this workgroup: lane butterfly, then waves in order.
   float pdn = dn_acc - dn_c, pdb = db_acc - db_c;
@@ -604,8 +633,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
     const float sdn = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
     const float sdb = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    p.partials[static_cast<int64_t>(bhk) * nkb + kb] = kLn2 * sdn;
-    p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = n * p.scale * sdb;
+    // the per-lane sums hold -dn and -db terms
+    p.partials[static_cast<int64_t>(bhk) * nkb + kb] = -kLn2 * sdn;
+    p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = -(n * p.scale) * sdb;
   }
 }
 
@@ -870,7 +900,8 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   auto issue_ds = [&](int t) {
     const uint32_t dst = lds_ds + (t % NDS) * DSTAGE + wave * 4096;
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) dma_buffer16(dst + s4 * 1024, ds_rsrc, ds_src, min(4 * t + s4, kj_max) * 1024);
+    // dS' is read exactly once: streaming cache policy
+    for (int s4 = 0; s4 < 4; ++s4) dma_buffer16<true>(dst + s4 * 1024, ds_rsrc, ds_src, min(4 * t + s4, kj_max) * 1024);
   };
 
   f32x16 dq[ND32];
@@ -921,7 +952,8 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   }
   wait_vm<0>();  // no direct-to-LDS load may outlive the workgroup
 
-  const float qscale = p.scale * *p.n_ptr * *p.b_ptr;
+  // the workspace holds -dS' (the dK/dV kernel's sign convention)
+  const float qscale = -(p.scale * *p.n_ptr * *p.b_ptr);
   if (qrow < N) {
     T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + qrow * p.dq.ss;
 #pragma unroll

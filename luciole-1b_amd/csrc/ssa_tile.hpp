@@ -92,11 +92,19 @@ __device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
 }
 
 // 16 bytes per lane from rsrc.base + voff + soff to LDS [m0 + 16 lane].
+// NT: non-temporal (streaming) cache policy, for data read exactly once.
+template <bool NT = false>
 __device__ __forceinline__ void dma_buffer16(uint32_t lds, const i32x4_t& rsrc, uint32_t voff, int soff) {
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "{m0}"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory");
+  if constexpr (NT)
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :
+                 : "{m0}"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory");
+  else
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "{m0}"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory");
 }
 
 // 16 bytes per lane from a per-lane global address to LDS [m0 + 16 lane].
@@ -128,6 +136,26 @@ __device__ __forceinline__ void store_b64(void* p, u32x2 v) {
 template <int OFF>
 __device__ __forceinline__ void buffer_store_b64(const i32x4_t& rs, uint32_t voff, int soff, u32x2 v) {
   asm volatile("s_nop 4\n\tbuffer_store_dwordx2 %0, %1, %2, %3 offen offset:%4"
+               :
+               : "v"(v), "v"(voff), "s"(rs), "s"(soff), "i"(OFF)
+               : "memory");
+}
+
+// 16 bytes per lane with the non-temporal (streaming) cache policy, one
+// vector-memory instruction each (as store_b64 / buffer_store_b64): for data
+// written once and read back once by a later kernel, so that it does not
+// evict reused tiles from L2.  A store of more than 8 bytes must not have its
+// data registers overwritten by the very next instruction: the trailing
+// s_nop 0 keeps that wait state inside the statement.
+template <int OFF>
+__device__ __forceinline__ void store_b128_nt(void* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off offset:%2 nt\n\ts_nop 0" : : "v"(reinterpret_cast<uint64_t>(p)),
+               "v"(v), "i"(OFF)
+               : "memory");
+}
+template <int OFF>
+__device__ __forceinline__ void buffer_store_b128_nt(const i32x4_t& rs, uint32_t voff, int soff, u32x4 v) {
+  asm volatile("s_nop 4\n\tbuffer_store_dwordx4 %0, %1, %2, %3 offen offset:%4 nt\n\ts_nop 0"
                :
                : "v"(v), "v"(voff), "s"(rs), "s"(soff), "i"(OFF)
                : "memory");
