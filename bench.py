@@ -102,6 +102,146 @@ def measured_traffic(config):
     return out
 
 
+# SQ counter passes of `bench.py --pmc-pass` (rocprofv3 --pmc, one database per
+# pass), summarised per SSA kernel by `bench.py --counters-summary DB ...`.  The
+# counters are totals over the device: SQ_VALU_MFMA_BUSY_CYCLES sums matrix-core
+# busy cycles over SIMDs; GRBM_GUI_ACTIVE counts GPU cycles per XCD (8 on MI355X);
+# SQ_ACTIVE_INST_* / SQ_WAIT_* count per-wave quad-cycles.
+CUS, SIMDS, XCDS = 256, 1024, 8
+COUNTER_ROW = re.compile(r"^\|\s*`(ssa_\w+?)`\s*\|" + r"\s*([0-9.]+)\s*\|" * 12)
+
+
+def counters_summary(dbs):
+    """Markdown table of the SSA kernels' counters from rocprofv3 databases."""
+    import sqlite3
+    from collections import defaultdict
+
+    tot = defaultdict(lambda: defaultdict(float))
+    dur, gui_pass = {}, {}
+    for db in dbs:
+        con = sqlite3.connect(db)
+        rows = con.execute("select dispatch_id, kernel_name, counter_name, value, duration from counters_collection")
+        for d, k, c, v, du in rows:
+            m = re.search(r"(ssa_\w+?_kernel)", k)
+            if not m:
+                continue
+            name = m.group(1)
+            if c == "GRBM_GUI_ACTIVE":  # collected in every pass: keep one
+                gui_pass[(db, name)] = gui_pass.get((db, name), 0.0) + v
+            else:
+                tot[name][c] += v
+            dur[name] = du / 1e6
+    for (db, name), v in gui_pass.items():
+        tot[name]["GRBM_GUI_ACTIVE"] = max(tot[name]["GRBM_GUI_ACTIVE"], v)
+    lines = ["| kernel | ms | clock GHz | MFMA busy % | VALU busy % | VALU/MFMA | trans/MFMA | SALU/MFMA | "
+             "LDS/MFMA | issue % | wait-any % | wait-dep % | LDS data FIFO full % |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for name, c in tot.items():
+        gui = c.get("GRBM_GUI_ACTIVE", 0.0) / XCDS
+        if not gui:
+            continue
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        per = lambda key: c.get(key, 0.0) / mf if mf else 0.0  # noqa: E731
+        wave = c.get("SQ_ACTIVE_INST_ANY", 0.0) + c.get("SQ_WAIT_ANY", 0.0) + c.get("SQ_WAIT_INST_ANY", 0.0)
+        frac = lambda key: 100.0 * c.get(key, 0.0) / wave if wave else 0.0  # noqa: E731
+        lines.append(
+            f"| `{name}` | {dur.get(name, 0.0):.4f} | {gui / (dur.get(name, 1.0) * 1e6):.2f} | "
+            f"{100.0 * c.get('SQ_VALU_MFMA_BUSY_CYCLES', 0.0) / (SIMDS * gui):.1f} | "
+            f"{100.0 * 4 * c.get('SQ_ACTIVE_INST_VALU', 0.0) / (SIMDS * gui):.1f} | "
+            f"{(c.get('SQ_INSTS_VALU', 0.0) - mf) / mf if mf else 0.0:.2f} | {per('SQ_INSTS_VALU_TRANS_F32'):.2f} | "
+            f"{per('SQ_INSTS_SALU'):.2f} | {per('SQ_INSTS_LDS'):.2f} | {frac('SQ_ACTIVE_INST_ANY'):.1f} | "
+            f"{frac('SQ_WAIT_ANY'):.1f} | {frac('SQ_WAIT_INST_ANY'):.1f} | "
+            f"{100.0 * c.get('SQ_LDS_DATA_FIFO_FULL', 0.0) / (CUS * gui):.1f} |")
+    return "\n".join(lines)
+
+
+def _csv_rows(path):
+    import csv
+
+    with open(path, newline="") as f:
+        yield from csv.DictReader(f)
+
+
+def _ssa_name(kernel_name):
+    m = re.search(r"(ssa_\w+?_kernel)", kernel_name)
+    return m.group(1) if m else None
+
+
+def trace_summary(trace_csv):
+    """Markdown table of the SSA kernels in a rocprofv3 --kernel-trace CSV."""
+    import statistics
+
+    per = {}
+    for r in _csv_rows(trace_csv):
+        name = _ssa_name(r["Kernel_Name"])
+        if name:
+            per.setdefault(name, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in per.values())
+    lines = ["| kernel | calls | avg us | median us | min us | max us | share % |", "|---|---|---|---|---|---|---|"]
+    for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{name}` | {len(v)} | {sum(v) / len(v):.1f} | {statistics.median(v):.1f} | {min(v):.1f} | "
+                     f"{max(v):.1f} | {100.0 * sum(v) / total:.1f} |")
+    return "\n".join(lines)
+
+
+def traffic_summary(fetch_csv, write_csv, config="s4096"):
+    """Markdown table of HBM bytes per launch from FETCH_SIZE / WRITE_SIZE CSVs
+    of `--pmc-pass` runs, each scaled by the factor that makes the counter read
+    exactly COPY_MIB MiB on the calibration copy, next to the algorithmic bytes."""
+    B, Hq, Hkv, S, D, causal = CONFIGS[config]
+    t = B * Hq * S * D * 2          # one [B, Hq, S, D] tensor
+    tkv = B * Hkv * S * D * 2
+    rows = B * Hq * S * 4           # M or Delta
+    nq = (S + 31) // 32
+    ds = B * Hq * (nq * (nq + 1) if causal else 2 * nq * nq) * 1024
+    alg = {"ssa_fwd_kernel": 2 * t + 2 * tkv + rows, "ssa_bwd_preprocess_kernel": 2 * t + rows,
+           "ssa_bwd_dkdv_kernel": 2 * t + 4 * tkv + 2 * rows + ds, "ssa_bwd_dq_kernel": ds + tkv + t}
+    vals = {}
+    for which, path in (("fetch", fetch_csv), ("write", write_csv)):
+        per = {}
+        for r in _csv_rows(path):
+            per[(r["Dispatch_Id"], r["Kernel_Name"])] = per.get((r["Dispatch_Id"], r["Kernel_Name"]), 0.0) + float(
+                r["Counter_Value"])
+        copy = [v for (d, k), v in per.items() if "copyBuffer" in k]
+        scale = COPY_MIB * 1024 / copy[-1]
+        for (d, k), v in per.items():
+            name = _ssa_name(k)
+            if name:
+                name = "ssa_bwd_dq_kernel" if name.startswith("ssa_bwd_dq") else name
+                vals.setdefault(name, {})[which] = v * scale * 1024 / 1e6
+        vals.setdefault("_scale", {})[which] = scale
+    lines = [f"Calibration: FETCH_SIZE x{vals['_scale']['fetch']:.4f}, WRITE_SIZE x{vals['_scale']['write']:.4f} "
+             f"(the factors that make each read {COPY_MIB} MiB on the calibration copy).", "",
+             "| kernel | fetch MB | write MB | total MB | algorithmic MB | total / algorithmic |",
+             "|---|---|---|---|---|---|"]
+    for name in ("ssa_fwd_kernel", "ssa_bwd_preprocess_kernel", "ssa_bwd_dkdv_kernel", "ssa_bwd_dq_kernel"):
+        if name in vals:
+            f, w = vals[name].get("fetch", 0.0), vals[name].get("write", 0.0)
+            lines.append(f"| `{name}` | {f:.1f} | {w:.1f} | {f + w:.1f} | {alg[name] / 1e6:.1f} | "
+                         f"{(f + w) / (alg[name] / 1e6):.3f} |")
+    return "\n".join(lines)
+
+
+def measured_counters(config):
+    """Per-kernel co-bound figures from profiles/ssa_counters_<config>.md (the
+    table `bench.py --counters-summary` prints); {} when the file is absent."""
+    f = ROOT / "profiles" / f"ssa_counters_{config}.md"
+    if not f.exists():
+        return {}
+    keys = ("counter_ms", "clock_ghz", "mfma_busy", "valu_busy", "valu_per_mfma", "trans_per_mfma",
+            "salu_per_mfma", "lds_per_mfma", "issue", "wait_any", "wait_dep", "lds_fifo_full")
+    out = {}
+    for line in f.read_text().splitlines():
+        m = COUNTER_ROW.match(line)
+        if m:
+            vals = [float(x) for x in m.groups()[1:]]
+            d = dict(zip(keys, vals))
+            for k in ("mfma_busy", "valu_busy", "issue", "wait_any", "wait_dep", "lds_fifo_full"):
+                d[k] /= 100.0
+            out[m.group(1)] = d
+    return out
+
+
 def pairs_dense(B, Hq, S, causal):
     return B * Hq * (S * (S + 1) // 2 if causal else S * S)
 
@@ -199,10 +339,26 @@ def main():
     ap.add_argument("--kernel-iters", type=int, default=50, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
+    ap.add_argument("--counters-summary", nargs="+", metavar="DB",
+                    help="print the per-kernel counter table of rocprofv3 --pmc databases of --pmc-pass runs "
+                         "(the table of profiles/ssa_counters_<config>.md) and exit")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="print the SSA kernel table of a rocprofv3 --kernel-trace CSV and exit")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM traffic table of FETCH_SIZE / WRITE_SIZE CSVs of --pmc-pass runs and exit")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="run each kernel of one step once, then a plain copy of COPY_MIB MiB "
                          "(counter calibration), and exit; for rocprofv3 --pmc runs")
     args = ap.parse_args()
+    if args.counters_summary:
+        print(counters_summary(args.counters_summary))
+        return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return
+    if args.traffic_summary:
+        print(traffic_summary(*args.traffic_summary, config=args.config))
+        return
     train = args.config in TRAIN_CONFIGS
     if args.steps is None:
         args.steps = 5 if train else 50
@@ -318,14 +474,32 @@ def main():
             kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
             kd["bound"] = "hbm"
     traffic = measured_traffic(args.config) if args.dtype == "bf16" else {}
+    counters = measured_counters(args.config) if args.dtype == "bf16" else {}
+    hip_name = {"ssa_bwd_dq_kernel": "ssa_bwd_dq_ds_kernel" if ds_bytes else "ssa_bwd_dq_kernel",
+                "ssa_bwd_reduce_kernel": "ssa_reduce_partials_kernel"}
     for name, kd in kernels.items():
         kd["hbm_bytes"] = traffic.get(name)
+        kd["counters"] = counters.get(hip_name.get(name, name))
     dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
     kd = kernels[dominant]
     if kd.get("bound") == "mfma":
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": kd["tflops"] / PEAK_BF16_TFLOPS, "traffic": kd["hbm_bytes"],
                     "avg_launch_ms": kd["avg_ms"]}
+        cn = kd.get("counters")
+        if cn:
+            # The SSA element work is the co-bound: the counters say what limits
+            # the kernel below the MFMA roofline (matrix-core and VALU busy
+            # fractions per SIMD at the measured clock, instructions per MFMA,
+            # and the share of wave time spent waiting).
+            roofline["co_bound"] = {
+                "mfma_busy": cn["mfma_busy"], "valu_busy": cn["valu_busy"],
+                "valu_per_mfma": cn["valu_per_mfma"], "trans_per_mfma": cn["trans_per_mfma"],
+                "salu_per_mfma": cn["salu_per_mfma"], "wait_frac": cn["wait_any"] + cn["wait_dep"],
+                "clock_ghz": cn["clock_ghz"],
+                "limiter": "issue and latency: neither the matrix core nor the VALU is saturated; the waves "
+                           "wait on operand reads, dependencies and the per-step barrier",
+                "source": f"profiles/ssa_counters_{args.config}.md"}
     else:
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": kd["gbps"], "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": kd["hbm_bytes"],
