@@ -34,15 +34,15 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 5
+#define SSA_ABI_VERSION 6
 
 /* Status codes. */
 enum {
   SSA_OK = 0,
   SSA_ERR_NULL_POINTER = 1,   /* a required pointer is NULL                       */
   SSA_ERR_SHAPE = 2,          /* bad batch/heads/seqlen (e.g. Hq % Hkv != 0)      */
-  SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128                  */
-  SSA_ERR_DTYPE = 4,          /* dtype not SSA_DTYPE_BF16 / SSA_DTYPE_FP16        */
+  SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128 (fp32: also 16)  */
+  SSA_ERR_DTYPE = 4,          /* dtype not an SSA_DTYPE_* (decode: bf16 / fp16)   */
   SSA_ERR_ALIGNMENT = 5,      /* layout: base pointer not 16-byte aligned, a      */
                               /* stride negative or not a multiple of 8, or the   */
                               /* row stride >= 2^24 elements                      */
@@ -52,8 +52,16 @@ enum {
                               /* exceed SSA_NOALLOC_SCRATCH_BYTES                 */
 };
 
-/* Element types of q/k/v/out/dout/dq/dk/dv. */
-enum { SSA_DTYPE_BF16 = 0, SSA_DTYPE_FP16 = 1 };
+/*
+ * Element types of q/k/v/out/dout/dq/dk/dv.  bf16 / fp16 run on the MFMA
+ * kernels (head dims 32, 64, 128).  fp32 -- the reference's fp32-operand path
+ * (training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:766-772, 819-825)
+ * -- runs on fp32 vector-ALU kernels (head dims 16, 32, 64, 128) that keep
+ * every product in fp32: full precision, a fraction of the bf16 throughput;
+ * with it the dS' workspace is not used (dq recomputes the scores) and the
+ * decode step is not offered.
+ */
+enum { SSA_DTYPE_BF16 = 0, SSA_DTYPE_FP16 = 1, SSA_DTYPE_FP32 = 2 };
 
 /* A [B, H, S, D] tensor view; strides in elements, stride(D) == 1. */
 typedef struct ssa_tensor4 {

@@ -26,6 +26,7 @@ SSA_ERR_SCRATCH = 8
 
 SSA_DTYPE_BF16 = 0
 SSA_DTYPE_FP16 = 1
+SSA_DTYPE_FP32 = 2
 
 # Every exported symbol of include/ssa_mi355x.h.
 EXPORTED_SYMBOLS = (
@@ -54,7 +55,7 @@ EXPORTED_SYMBOLS = (
     "ssa_cross_entropy",
 )
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class Tensor4(ctypes.Structure):

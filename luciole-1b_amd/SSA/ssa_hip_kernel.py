@@ -27,9 +27,15 @@ a transient workspace so that dQ is one streaming product with K instead of
 the reference's recompute of the scores (measured faster at D = 128, slower at
 D = 64, where the recompute is cheap); ``SSA_BWD_DS=0`` / ``1`` forces either
 path, and a workspace above ``SSA_BWD_DS_MAX_BYTES`` (default 16 GiB) always
-recomputes.  Errors: ``AssertionError`` for ``Hq % Hkv != 0`` and a
-non-power-of-two head dim, as in the reference; ``ValueError`` for head dims
-other than 32/64/128 and dtypes other than bf16/fp16.
+recomputes.  Head dims 32, 64 and 128 run on kernels of their own; in bf16 /
+fp16, head dim 16 (the smallest the reference's Triton kernel takes) runs on
+the D = 32 kernels with its operands zero-padded to 32 columns, which changes
+no score, dP or Delta, and the results are sliced back (the decode step is not
+offered at D = 16).  fp32 inputs (the reference's fp32-operand path) run on
+fp32 vector-ALU kernels for head dims 16-128 that keep every product in fp32,
+without the dS' workspace; the decode step takes bf16 / fp16 only.  Errors:
+``AssertionError`` for ``Hq % Hkv != 0`` and a non-power-of-two head dim, as in
+the reference; ``ValueError`` for other head dims and other dtypes.
 """
 
 from __future__ import annotations
@@ -41,7 +47,8 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.bfloat16: _lib.SSA_DTYPE_BF16, torch.float16: _lib.SSA_DTYPE_FP16}
+_DTYPES = {torch.bfloat16: _lib.SSA_DTYPE_BF16, torch.float16: _lib.SSA_DTYPE_FP16,
+           torch.float32: _lib.SSA_DTYPE_FP32}
 
 
 def _is_pow2(x: int) -> bool:
@@ -77,6 +84,15 @@ def _scalar(x, device) -> torch.Tensor:
     return torch.tensor(float(x), dtype=torch.float32, device=device)
 
 
+# Head dims that run on the kernels of a wider one, with zero-padded columns.
+_PADDED_HEAD_DIM = {16: 32}
+
+
+def _pad_cols(t: torch.Tensor, width: int) -> torch.Tensor:
+    """``t`` with its last dim zero-padded to ``width`` (a new contiguous tensor)."""
+    return torch.nn.functional.pad(t, (0, width - t.shape[-1]))
+
+
 def _check_inputs(q, k, v):
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be 4-D [B, H, N, D] tensors")
@@ -87,7 +103,7 @@ def _check_inputs(q, k, v):
     if tuple(k.shape) != (B, Hkv, N, D) or tuple(v.shape) != (B, Hkv, N, D):
         raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
     if q.dtype not in _DTYPES:
-        raise ValueError(f"unsupported dtype {q.dtype}: the MI355X SSA kernels take bf16 or fp16")
+        raise ValueError(f"unsupported dtype {q.dtype}: the MI355X SSA kernels take bf16, fp16 or fp32")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k, v must share one dtype")
     if not (q.is_cuda and k.device == q.device and v.device == q.device):
@@ -95,9 +111,19 @@ def _check_inputs(q, k, v):
     return B, Hq, Hkv, N, D
 
 
+def _padded_width(D: int, dtype: torch.dtype) -> int:
+    """Head dim whose bf16 / fp16 kernels run head dim D zero-padded, or 0 (fp32 has its own D = 16 kernels)."""
+    return 0 if dtype == torch.float32 else _PADDED_HEAD_DIM.get(D, 0)
+
+
 def ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True):
     """SSA attention forward.  Returns ``(out [B,Hq,N,D], m [B,Hq,N] fp32)``."""
     B, Hq, Hkv, N, D = _check_inputs(q, k, v)
+    w = _padded_width(D, q.dtype)
+    if w:
+        out, m = ssa_flash_attn_forward(_pad_cols(q, w), _pad_cols(k, w), _pad_cols(v, w), softmax_scale, ssa_n,
+                                        ssa_b, causal)
+        return out[..., :D].contiguous(), m
     q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
     n32 = _scalar(ssa_n, q.device)
     b32 = _scalar(ssa_b, q.device)
@@ -165,8 +191,9 @@ class BackwardLaunch:
         self.dn = torch.empty((), device=dev, dtype=torch.float32)
         self.db = torch.empty((), device=dev, dtype=torch.float32)
         ds_bytes = int(self.lib.ssa_bwd_ds_workspace_bytes(B, Hq, N, int(bool(causal))))
+        # fp32 has no dS' workspace path (its dq always recomputes)
         self.ds = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-                   if _use_ds_workspace(ds_bytes, D, ds) else None)
+                   if q.dtype != torch.float32 and _use_ds_workspace(ds_bytes, D, ds) else None)
         self.device = dev
         self.args = _lib.BwdArgs(
             _t4(self.q), _t4(self.k), _t4(self.v), _t4(self.out), _t4(self.dout),
@@ -199,6 +226,13 @@ class BackwardLaunch:
 def ssa_flash_attn_backward(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal=True, ds=None):
     """SSA attention backward.  Returns ``(dq, dk, dv, dn, db)``; dn/db are 0-d fp32 tensors.
     ``ds``: keep dS' in a workspace (True / False; None: the ``SSA_BWD_DS`` policy)."""
+    D = q.shape[-1] if q.dim() == 4 else 0
+    w = _padded_width(D, q.dtype)
+    if w and tuple(out.shape) == tuple(q.shape) and tuple(dout.shape) == tuple(q.shape):
+        dq, dk, dv, dn, db = ssa_flash_attn_backward(
+            _pad_cols(q, w), _pad_cols(k, w), _pad_cols(v, w), _pad_cols(out, w), _pad_cols(dout, w), m,
+            softmax_scale, ssa_n, ssa_b, causal, ds)
+        return dq[..., :D].contiguous(), dk[..., :D].contiguous(), dv[..., :D].contiguous(), dn, db
     launch = BackwardLaunch(q, k, v, out, dout, m, softmax_scale, ssa_n, ssa_b, causal, ds)
     launch.run()
     return launch.results()
@@ -209,7 +243,7 @@ def ssa_bwd_preprocess(out, dout):
     if out.dim() != 4 or tuple(dout.shape) != tuple(out.shape):
         raise ValueError("out and dout must be matching [B, H, N, D] tensors")
     if out.dtype not in _DTYPES or dout.dtype != out.dtype:
-        raise ValueError("out/dout must be bf16 or fp16 with one dtype")
+        raise ValueError("out/dout must be bf16, fp16 or fp32 with one dtype")
     B, H, N, D = out.shape
     out, dout = _kernel_layout(out), _kernel_layout(dout)
     delta = torch.empty((B, H, N), device=out.device, dtype=torch.float32)
@@ -260,7 +294,7 @@ def _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen):
     if tuple(k.shape) != (T, Hkv, D) or tuple(v.shape) != (T, Hkv, D):
         raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("q, k, v must share one dtype, bf16 or fp16")
+        raise ValueError("q, k, v must share one dtype, bf16, fp16 or fp32")
     if not (q.is_cuda and k.device == q.device and v.device == q.device):
         raise ValueError("q, k, v must be on the same GPU device")
     if not torch.is_tensor(cu_seqlens) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
@@ -275,6 +309,11 @@ def ssa_flash_attn_varlen_forward(q, k, v, cu_seqlens, max_seqlen, softmax_scale
     (int32, on the device), max_seqlen = longest document.  Returns
     ``(out [T,Hq,D], m [Hq,T] fp32)``."""
     cu, docs, T, Hq, Hkv, D, max_seqlen = _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen)
+    w = _padded_width(D, q.dtype)
+    if w:
+        out, m = ssa_flash_attn_varlen_forward(_pad_cols(q, w), _pad_cols(k, w), _pad_cols(v, w), cu, max_seqlen,
+                                               softmax_scale, ssa_n, ssa_b, causal)
+        return out[..., :D].contiguous(), m
     q, k, v = _thd_layout(q), _thd_layout(k), _thd_layout(v)
     n32 = _scalar(ssa_n, q.device)
     b32 = _scalar(ssa_b, q.device)
@@ -299,6 +338,12 @@ def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen
     cu, docs, T, Hq, Hkv, D, max_seqlen = _check_varlen_inputs(q, k, v, cu_seqlens, max_seqlen)
     if tuple(out.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape) or out.dtype != q.dtype:
         raise ValueError("out and dout must have the shape (and out the dtype) of q")
+    w = _padded_width(D, q.dtype)
+    if w:
+        dq, dk, dv, dn, db = ssa_flash_attn_varlen_backward(
+            _pad_cols(q, w), _pad_cols(k, w), _pad_cols(v, w), _pad_cols(out, w), _pad_cols(dout, w), m, cu,
+            max_seqlen, softmax_scale, ssa_n, ssa_b, causal, ds)
+        return dq[..., :D].contiguous(), dk[..., :D].contiguous(), dv[..., :D].contiguous(), dn, db
     q, k, v = _thd_layout(q), _thd_layout(k), _thd_layout(v)
     out, dout = _thd_layout(out), _thd_layout(dout.to(q.dtype))
     m = m.to(torch.float32).contiguous()
@@ -318,7 +363,7 @@ def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen
     db = torch.empty((), device=dev, dtype=torch.float32)
     ds_bytes = int(lib.ssa_varlen_bwd_ds_workspace_bytes(docs, Hq, max_seqlen, T, int(bool(causal))))
     ds_ws = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-             if ds_bytes > 0 and _use_ds_workspace(ds_bytes, D, ds) else None)
+             if ds_bytes > 0 and q.dtype != torch.float32 and _use_ds_workspace(ds_bytes, D, ds) else None)
     dense = _lib.BwdArgs(
         _t3(q), _t3(k), _t3(v), _t3(out), _t3(dout), _t3(dq), _t3(dk), _t3(dv),
         m.data_ptr(), delta.data_ptr(), partials.data_ptr(), dn.data_ptr(), db.data_ptr(),
@@ -400,8 +445,8 @@ def ssa_decode_attention(q, k_cache, v_cache, cache_seqlens, softmax_scale, ssa_
     assert _is_pow2(D), f"Head dim D={D} must be a power of two"
     if tuple(k_cache.shape) != (B, Hkv, cap, D) or tuple(v_cache.shape) != (B, Hkv, cap, D):
         raise ValueError(f"cache shapes {tuple(k_cache.shape)}/{tuple(v_cache.shape)} do not match q {tuple(q.shape)}")
-    if q.dtype not in _DTYPES:
-        raise ValueError(f"unsupported dtype {q.dtype}: the MI355X SSA kernels take bf16 or fp16")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"unsupported dtype {q.dtype}: the decode step takes bf16 or fp16")
     if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
         raise ValueError("q and the caches must share one dtype")
     if not (q.is_cuda and k_cache.device == q.device and v_cache.device == q.device):

@@ -30,8 +30,8 @@ int32_t check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t N, int32_t D, i
   if (Hq % Hkv != 0) return SSA_ERR_SHAPE;
   // Grid sizes are int32 block counts; keep every product well inside range.
   if (static_cast<int64_t>(B) * Hq * ((static_cast<int64_t>(N) + 127) / 128) > (1ll << 30)) return SSA_ERR_SHAPE;
-  if (D != 32 && D != 64 && D != 128) return SSA_ERR_HEAD_DIM;
-  if (dtype != SSA_DTYPE_BF16 && dtype != SSA_DTYPE_FP16) return SSA_ERR_DTYPE;
+  if (dtype != SSA_DTYPE_BF16 && dtype != SSA_DTYPE_FP16 && dtype != SSA_DTYPE_FP32) return SSA_ERR_DTYPE;
+  if (D != 32 && D != 64 && D != 128 && !(D == 16 && dtype == SSA_DTYPE_FP32)) return SSA_ERR_HEAD_DIM;
   return SSA_OK;
 }
 
@@ -165,8 +165,8 @@ const char* ssa_status_string(int32_t status) {
     case SSA_OK: return "ok";
     case SSA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case SSA_ERR_SHAPE: return "invalid shape (batch/heads/seqlen must be > 0 and Hq % Hkv == 0)";
-    case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128)";
-    case SSA_ERR_DTYPE: return "unsupported dtype (supported: bf16, fp16)";
+    case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128; fp32 also 16)";
+    case SSA_ERR_DTYPE: return "unsupported dtype (supported: bf16, fp16, fp32; the decode step bf16, fp16)";
     case SSA_ERR_ALIGNMENT:
       return "unsupported tensor layout (base pointer 16-byte aligned, strides non-negative multiples of 8 "
              "elements, row stride below 2^24 elements)";
@@ -275,6 +275,7 @@ int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* va, void* stream) {
   f.T = va->total_tokens;
   f.Nmax = a->seqlen;
   f.D = a->head_dim;
+  f.esize = a->dtype == SSA_DTYPE_FP32 ? 4 : 2;
   return launch_status(ssa::launch_varlen_fill(f, s));
 }
 
@@ -309,6 +310,7 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   f.T = va->total_tokens;
   f.Nmax = a->seqlen;
   f.D = a->head_dim;
+  f.esize = a->dtype == SSA_DTYPE_FP32 ? 4 : 2;
   return launch_status(ssa::launch_varlen_fill(f, s));
 }
 

@@ -7,7 +7,8 @@
 
 namespace ssa {
 
-// dtype: 0 = bf16, 1 = fp16.  D in {32, 64, 128} (validated by the caller).
+// dtype: 0 = bf16, 1 = fp16 (D in {32, 64, 128}), 2 = fp32 (D in {16, 32, 64,
+// 128}, the vector-ALU kernels of ssa_f32.hip); validated by the caller.
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
 hipError_t launch_bwd_preprocess(const BwdParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
@@ -15,6 +16,13 @@ hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, bool causal, hipS
 hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t stream);
+
+// fp32 inputs (ssa_f32.hip); the dS' workspace is not used (dQ recomputes).
+constexpr int kDtypeF32 = 2;
+hipError_t launch_fwd_f32(const FwdParams& p, int D, bool causal, hipStream_t stream);
+hipError_t launch_bwd_preprocess_f32(const BwdParams& p, int D, hipStream_t stream);
+hipError_t launch_bwd_dkdv_f32(const BwdParams& p, int D, bool causal, hipStream_t stream);
+hipError_t launch_bwd_dq_f32(const BwdParams& p, int D, bool causal, hipStream_t stream);
 
 }  // namespace ssa
 
@@ -29,8 +37,8 @@ int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_onl
 int32_t run_bwd(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s);
 
 // Packed batches: write the token rows no document covers (ssa_varlen_fill.hip):
-// up to three [T, H, D] bf16/fp16 tensors (rows set to 0) and optionally an
-// [m_heads, T] fp32 normaliser (set to -inf).
+// up to three [T, H, D] tensors of esize-byte elements (rows set to 0) and
+// optionally an [m_heads, T] fp32 normaliser (set to -inf).
 struct VarlenFill {
   Tensor4 t[3];
   int heads[3];
@@ -39,6 +47,7 @@ struct VarlenFill {
   int m_heads;
   const int* cu;
   int B, T, Nmax, D;
+  int esize;  // bytes per element: 2 (bf16 / fp16) or 4 (fp32)
 };
 hipError_t launch_varlen_fill(const VarlenFill& f, hipStream_t stream);
 

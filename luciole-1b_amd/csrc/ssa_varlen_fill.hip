@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void ssa_varlen_fill_kernel(VarlenFill f) {
   }
   if (a >= e) return;
   const int rows = e - a;
-  const int cpr = f.D / 8;  // 16-byte chunks per (token, head) row
+  const int cpr = f.D * f.esize / 16;  // 16-byte chunks per (token, head) row
   for (int j = 0; j < f.ntensors; ++j) {
     const Tensor4& t = f.t[j];
     const int H = f.heads[j];
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void ssa_varlen_fill_kernel(VarlenFill f) {
       const int64_t th = it / cpr;
       const int h = static_cast<int>(th % H);
       const int tok = a + static_cast<int>(th / H);
-      char* p = static_cast<char*>(const_cast<void*>(t.ptr)) + ((tok * t.ss + h * t.sh) * 2 + c * 16);
+      char* p = static_cast<char*>(const_cast<void*>(t.ptr)) + ((tok * t.ss + h * t.sh) * f.esize + c * 16);
       *reinterpret_cast<u32x4*>(p) = u32x4{0u, 0u, 0u, 0u};
     }
   }

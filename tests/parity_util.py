@@ -9,6 +9,9 @@ Pass bar, per tensor, against the unrounded fp64 oracle:
     (training/train/train_ssa_triton/check_ssa_triton_parity.py:124-149,206,
     219-237, tolerances :1060-1069);
   * dn / db: |got - ref| <= 2e-3 + 2e-2 |ref| (the reference's scalar bar).
+fp32 tensors take the reference's fp32 bars instead: allclose(atol=5e-4,
+rtol=1e-3) against the unrounded oracle for every element, and
+|got - ref| <= 5e-5 + 1e-4 |ref| for dn / db (the same lines).
 The reported "max_abs" is the plain maximum |got - ref|.
 """
 
@@ -27,6 +30,9 @@ MAX_ABS = 2e-2
 # (check_ssa_triton_parity.py:1060-1069).
 ATOL, RTOL = 2e-2, 5e-2
 SCALAR_ATOL, SCALAR_RTOL = 2e-3, 2e-2
+# fp32 operands (check_ssa_triton_parity.py:1064-1065, 1068-1069)
+ATOL_F32, RTOL_F32 = 5e-4, 1e-3
+SCALAR_ATOL_F32, SCALAR_RTOL_F32 = 5e-5, 1e-4
 
 
 def make_inputs(B, Hq, Hkv, N, D, dtype, device, layout="contig", seed=1234, qkv_scale=1.0):
@@ -75,34 +81,41 @@ def tensor_err(got: torch.Tensor, ref: np.ndarray) -> dict:
     r = torch.from_numpy(np.ascontiguousarray(ref)).float()
     r_round = r.to(got.dtype).float() if got.dtype in (torch.bfloat16, torch.float16) else r
     d_raw = (g - r).abs()
-    bound = torch.maximum(torch.full_like(r, MAX_ABS), ulp(r, got.dtype))
+    if got.dtype == torch.float32:
+        bound = ATOL_F32 + RTOL_F32 * r.abs()
+        atol, rtol = ATOL_F32, RTOL_F32
+    else:
+        bound = torch.maximum(torch.full_like(r, MAX_ABS), ulp(r, got.dtype))
+        atol, rtol = ATOL, RTOL
     return {
         "max_abs": float(d_raw.max()) if d_raw.numel() else 0.0,
         "max_abs_vs_rounded": float((g - r_round).abs().max()) if d_raw.numel() else 0.0,
         "within_bound": bool((d_raw <= bound).all()),
         "rel_rmse": float(torch.sqrt(((g - r) ** 2).mean()) / (torch.sqrt((r ** 2).mean()) + 1e-12)),
-        "allclose": bool(torch.allclose(g, r_round, atol=ATOL, rtol=RTOL)),
+        "allclose": bool(torch.allclose(g, r_round, atol=atol, rtol=rtol)),
         "finite": bool(torch.isfinite(g).all()),
     }
 
 
-def scalar_err(got, ref: float) -> dict:
+def scalar_err(got, ref: float, fp32: bool = False) -> dict:
     gv = float(got)
     diff = abs(gv - ref)
+    atol, rtol = (SCALAR_ATOL_F32, SCALAR_RTOL_F32) if fp32 else (SCALAR_ATOL, SCALAR_RTOL)
     return {
         "got": gv,
         "ref": ref,
         "abs_diff": diff,
         "rel": diff / max(abs(ref), 1e-12),
-        "allclose": diff <= SCALAR_ATOL + SCALAR_RTOL * abs(ref),
+        "allclose": diff <= atol + rtol * abs(ref),
     }
 
 
 def compare(outs: dict, ref: dict, names=("out", "dq", "dk", "dv"), scalars=("dn", "db")) -> dict:
     res = {name: tensor_err(outs[name], ref[name]) for name in names if name in outs}
+    fp32 = any(outs[name].dtype == torch.float32 for name in res)
     for name in scalars:
         if name in outs:
-            res[name] = scalar_err(outs[name], ref[name])
+            res[name] = scalar_err(outs[name], ref[name], fp32)
     return res
 
 
@@ -112,7 +125,7 @@ def assert_parity(res: dict, label: str) -> None:
             assert st["allclose"], f"{label}: {name} {st}"
             continue
         assert st["finite"], f"{label}: {name} has non-finite values"
-        assert st["within_bound"], f"{label}: {name} exceeds max(2e-2, 1 ulp) ({st})"
+        assert st["within_bound"], f"{label}: {name} exceeds its per-element bound ({st})"
         assert st["allclose"], f"{label}: {name} not allclose ({st})"
 
 

@@ -135,6 +135,7 @@ def _bwd_args(**kw):
         ("seqlen", 0, _lib.SSA_ERR_SHAPE),
         ("head_dim", 96, _lib.SSA_ERR_HEAD_DIM),
         ("head_dim", 256, _lib.SSA_ERR_HEAD_DIM),
+        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),    # bf16: D = 16 runs padded in Python, not here
         ("dtype", 7, _lib.SSA_ERR_DTYPE),
         ("m", None, _lib.SSA_ERR_NULL_POINTER),
         ("ssa_n", None, _lib.SSA_ERR_NULL_POINTER),
@@ -150,6 +151,15 @@ def test_fwd_validation(field, value, status):
     assert _lib.lib().ssa_fwd(ctypes.byref(a), None) == status
 
 
+def test_fp32_head_dims():
+    """fp32 takes head dims 16..128 (powers of two); other head dims stay refused."""
+    for D in (48, 96, 256, 8):
+        a = _fwd_args(dtype=_lib.SSA_DTYPE_FP32, head_dim=D)
+        assert _lib.lib().ssa_fwd(ctypes.byref(a), None) == _lib.SSA_ERR_HEAD_DIM, D
+        b = _bwd_args(dtype=_lib.SSA_DTYPE_FP32, head_dim=D)
+        assert _lib.lib().ssa_bwd(ctypes.byref(b), None) == _lib.SSA_ERR_HEAD_DIM, D
+
+
 def test_fwd_null_args():
     assert _lib.lib().ssa_fwd(None, None) == _lib.SSA_ERR_NULL_POINTER
 
@@ -159,8 +169,8 @@ def test_fwd_null_args():
     "field,value,status",
     [
         ("heads_kv", 5, _lib.SSA_ERR_SHAPE),
-        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),
-        ("dtype", 2, _lib.SSA_ERR_DTYPE),
+        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),    # D = 16 only with fp32
+        ("dtype", 3, _lib.SSA_ERR_DTYPE),
         ("partials", None, _lib.SSA_ERR_NULL_POINTER),
         ("dn", None, _lib.SSA_ERR_NULL_POINTER),
         ("dq", _lib.Tensor4(FAKE, 4, 0, 128), _lib.SSA_ERR_ALIGNMENT),
@@ -263,6 +273,7 @@ def _decode_args(**kw):
         ("num_splits", -2, _lib.SSA_ERR_SHAPE),
         ("head_dim", 48, _lib.SSA_ERR_HEAD_DIM),
         ("dtype", 3, _lib.SSA_ERR_DTYPE),
+        ("dtype", _lib.SSA_DTYPE_FP32, _lib.SSA_ERR_DTYPE),   # decode: bf16 / fp16 only
         ("cache_seqlens", None, _lib.SSA_ERR_NULL_POINTER),
         ("ssa_b", None, _lib.SSA_ERR_NULL_POINTER),
         ("workspace", None, _lib.SSA_ERR_NULL_POINTER),   # 4 x 8 heads x 4096 keys needs splits
@@ -356,8 +367,8 @@ def test_cross_entropy_validation():
     "field,value,status",
     [
         ("heads_kv", 5, _lib.SSA_ERR_SHAPE),
-        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),
-        ("dtype", 2, _lib.SSA_ERR_DTYPE),
+        ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),    # D = 16 only with fp32
+        ("dtype", 3, _lib.SSA_ERR_DTYPE),
         ("dn", None, _lib.SSA_ERR_NULL_POINTER),
         ("m", None, _lib.SSA_ERR_NULL_POINTER),
         ("dq", _lib.Tensor4(FAKE, 4, 0, 128), _lib.SSA_ERR_ALIGNMENT),

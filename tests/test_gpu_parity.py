@@ -3,8 +3,9 @@
 Mirrors the reference kernel suite (training/train/train_ssa_triton/
 check_ssa_triton_parity.py:295-504): kernel-level ssa_flash_attn_forward /
 ssa_flash_attn_backward on seeded inputs, contiguous and Megatron-strided
-layouts, MHA and GQA, causal and non-causal, bf16 and fp16 -- extended to
-D in {32, 64, 128}, ragged N, and trained values of n.
+layouts, MHA and GQA, causal and non-causal, bf16, fp16 and fp32 (the last
+at the reference's fp32 tolerances) -- extended to D in {16, 32, 64, 128},
+ragged N, and trained values of n.
 """
 
 from __future__ import annotations
@@ -57,7 +58,7 @@ def _run(gpu, B, Hq, Hkv, N, D, dtype, causal, layout="contig", n_val=1.5, b_val
 
 
 def _check(label, res_exact, res_kernel, mres):
-    assert mres < 1e-2, f"{label}: m max abs {mres}"
+    assert mres < (1e-4 if "float32" in label else 1e-2), f"{label}: m max abs {mres}"
     assert_parity(res_exact, label + " [exact]")
     assert_parity(res_kernel, label + " [kernel-level]")
 
@@ -69,6 +70,45 @@ def _check(label, res_exact, res_kernel, mres):
 @pytest.mark.parametrize("dq_path", ["ds", "recompute"])
 def test_parity_matrix(gpu, D, dtype, causal, heads, dq_path):
     _check(*_run(gpu, 1, heads[0], heads[1], 256, D, dtype, causal, ds=dq_path == "ds"))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("heads", [(4, 4), (8, 2)])
+@pytest.mark.parametrize("N", [7, 256])
+def test_parity_head_dim_16(gpu, dtype, causal, heads, N):
+    """Head dim 16 (the reference kernel's smallest): zero-padded onto the D = 32 kernels."""
+    _check(*_run(gpu, 1, heads[0], heads[1], N, 16, dtype, causal))
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("heads", [(4, 4), (8, 2)])
+@pytest.mark.parametrize("N", [7, 256])
+def test_parity_fp32(gpu, D, causal, heads, N):
+    """fp32 operands (the reference's fp32 path) on the fp32 vector-ALU kernels,
+    at the reference's fp32 tolerances (atol 5e-4, rtol 1e-3; dn / db 5e-5 + 1e-4 |ref|)."""
+    _check(*_run(gpu, 1, heads[0], heads[1], N, D, torch.float32, causal))
+
+
+@pytest.mark.parametrize("N", [1, 129, 511])
+@pytest.mark.parametrize("layout", ["contig", "strided"])
+def test_parity_fp32_ragged_strided(gpu, N, layout):
+    _check(*_run(gpu, 2, 4, 2, N, 64, torch.float32, True, layout=layout))
+
+
+def test_parity_fp32_trained_n(gpu):
+    _check(*_run(gpu, 1, 4, 4, 300, 128, torch.float32, False, n_val=4.0, qkv_scale=0.5))
+
+
+@pytest.mark.parametrize("D", [8, 256])
+def test_unsupported_head_dims_raise(gpu, D):
+    from SSA.ssa_triton_kernel import ssa_flash_attn_forward
+
+    q = torch.randn(1, 2, 64, D, dtype=torch.bfloat16, device=gpu)
+    n = torch.tensor(1.5, device=gpu)
+    with pytest.raises(ValueError):
+        ssa_flash_attn_forward(q, q, q, 1.0 / math.sqrt(D), n, n, causal=True)
 
 
 @pytest.mark.parametrize("N", [1, 7, 64, 129, 200, 511])

@@ -78,6 +78,7 @@ CASES = [
     ((300, 513), 2, 1, 128, True),
     ((129, 31, 200), 4, 2, 128, False),
     ((40, 90, 257), 2, 2, 32, True),
+    ((40, 90, 257), 4, 2, 16, True),  # head dim 16: zero-padded onto the D = 32 kernels
 ]
 
 
@@ -162,19 +163,33 @@ def test_varlen_malformed_table_is_clamped(gpu, ds):
     assert_parity(res, "clamped table")
 
 
-@pytest.mark.parametrize("ds", [False, True], ids=["recompute", "ds"])
-def test_varlen_uncovered_rows_are_written(gpu, ds):
+@pytest.mark.parametrize("lens,D,causal", [((5, 100, 33, 260, 1), 128, True), ((40, 90, 257), 16, False),
+                                           ((7, 1, 33), 64, True)])
+def test_varlen_fp32(gpu, lens, D, causal):
+    """fp32 token streams on the fp32 kernels, at the reference's fp32 tolerances."""
+    label = f"varlen fp32 lens={lens} D={D} causal={int(causal)}"
+    print(f"[gpu case] {label}", file=sys.stderr, flush=True)
+    q, k, v, do, cu = _inputs(lens, 4, 2, D, torch.float32, gpu)
+    _, _, _, res, res_k, merr = _run(gpu, q, k, v, do, cu, max(lens), causal)
+    assert merr < 1e-4, f"{label}: m {merr}"
+    assert_parity(res, label)
+    assert_parity(res_k, label + " [kernel-level]")
+
+
+@pytest.mark.parametrize("ds,dtype", [(False, torch.bfloat16), (True, torch.bfloat16), (False, torch.float32)],
+                         ids=["recompute", "ds", "fp32"])
+def test_varlen_uncovered_rows_are_written(gpu, ds, dtype):
     """Tokens in no document -- after cu[-1] < T, and the tail of a document
     longer than max_seqlen (cut to its first max_seqlen tokens) -- come back as
     out = 0, m = -inf and dq = dk = dv = 0, never as stale memory: the caching
     allocator is first filled with NaN blocks of the output sizes, which the
     outputs then reuse."""
     lens_cover, T, max_seqlen = (37, 83), 200, 60   # covered: [0, 37), [37, 97); tokens 97..199 are not
-    label = f"varlen uncovered rows ds={int(ds)}"
+    label = f"varlen uncovered rows ds={int(ds)} {str(dtype)[6:]}"
     print(f"[gpu case] {label}", file=sys.stderr, flush=True)
     Hq, Hkv, D = 4, 2, 64
-    q, k, v, do, _ = _inputs((T,), Hq, Hkv, D, torch.bfloat16, gpu)
-    poison = [torch.full((T, h, D), float("nan"), device=gpu, dtype=torch.bfloat16) for h in (Hq, Hq, Hkv, Hkv)]
+    q, k, v, do, _ = _inputs((T,), Hq, Hkv, D, dtype, gpu)
+    poison = [torch.full((T, h, D), float("nan"), device=gpu, dtype=dtype) for h in (Hq, Hq, Hkv, Hkv)]
     poison.append(torch.full((Hq, T), float("nan"), device=gpu))
     del poison
     cu = torch.tensor([0, 37, 37 + 83], dtype=torch.int32)
