@@ -40,7 +40,11 @@ extern "C" {
 enum {
   SSA_OK = 0,
   SSA_ERR_NULL_POINTER = 1,   /* a required pointer is NULL                       */
-  SSA_ERR_SHAPE = 2,          /* bad batch/heads/seqlen (e.g. Hq % Hkv != 0)      */
+  SSA_ERR_SHAPE = 2,          /* bad batch/heads/seqlen (e.g. Hq % Hkv != 0), or  */
+                              /* beyond the int32 launch limits: seqlen <= 2^30,  */
+                              /* B * Hq * ceil(seqlen / 128) <= 2^28, and query   */
+                              /* rows B * Hq * seqlen (packed: Hq * total_tokens) */
+                              /* <= INT32_MAX; decode: capacity <= 2^30          */
   SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128 (fp32: also 16)  */
   SSA_ERR_DTYPE = 4,          /* dtype not an SSA_DTYPE_* (decode: bf16 / fp16)   */
   SSA_ERR_ALIGNMENT = 5,      /* layout: base pointer not 16-byte aligned, a      */

@@ -245,6 +245,9 @@ def ssa_bwd_preprocess(out, dout):
     if out.dtype not in _DTYPES or dout.dtype != out.dtype:
         raise ValueError("out/dout must be bf16, fp16 or fp32 with one dtype")
     B, H, N, D = out.shape
+    w = _padded_width(D, out.dtype)
+    if w:  # zero columns add nothing to the row sums
+        out, dout, D = _pad_cols(out, w), _pad_cols(dout, w), w
     out, dout = _kernel_layout(out), _kernel_layout(dout)
     delta = torch.empty((B, H, N), device=out.device, dtype=torch.float32)
     args = _lib.BwdArgs()

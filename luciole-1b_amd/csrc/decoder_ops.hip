@@ -313,6 +313,9 @@ extern "C" int32_t ssa_rope(const ssa_rope_args* a, void* stream) {
   if (a == nullptr || a->x == nullptr || a->y == nullptr || a->cos == nullptr || a->sin == nullptr)
     return SSA_OPS_ERR_NULL_POINTER;
   if (a->seqlen <= 0 || a->batch <= 0 || a->heads <= 0) return SSA_OPS_ERR_SHAPE;
+  // (token, head) rows fit int32, so the grid of head_dim / 8 threads per row fits too
+  const int64_t sb = static_cast<int64_t>(a->seqlen) * a->batch;
+  if (sb > INT32_MAX || sb * a->heads > INT32_MAX) return SSA_OPS_ERR_SHAPE;
   if (a->head_dim != 64 && a->head_dim != 128) return SSA_OPS_ERR_SHAPE;
   if (a->dtype != 0 && a->dtype != 1) return SSA_OPS_ERR_DTYPE;
   if (a->x_stride_s < 0 || a->x_stride_b < 0 || a->x_stride_h < 0) return SSA_OPS_ERR_ALIGNMENT;
@@ -327,7 +330,7 @@ extern "C" int32_t ssa_rope(const ssa_rope_args* a, void* stream) {
 
 extern "C" int64_t ssa_rmsnorm_workspace_floats(int32_t rows, int32_t hidden) {
   if (rows <= 0 || hidden <= 0) return 0;
-  return static_cast<int64_t>((rows + kNormBwdRows - 1) / kNormBwdRows) * hidden;
+  return (static_cast<int64_t>(rows) + kNormBwdRows - 1) / kNormBwdRows * hidden;
 }
 
 extern "C" int32_t ssa_rmsnorm_fwd(const ssa_rmsnorm_fwd_args* a, void* stream) {
@@ -356,7 +359,7 @@ extern "C" int32_t ssa_rmsnorm_bwd(const ssa_rmsnorm_bwd_args* a, void* stream) 
   if (a->dx == nullptr || a->dweight == nullptr || a->workspace == nullptr) return SSA_OPS_ERR_NULL_POINTER;
   if (!aligned(a->dx, 16) || !aligned(a->workspace, 16) || !aligned(a->dy, 8)) return SSA_OPS_ERR_ALIGNMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nparts = (a->rows + kNormBwdRows - 1) / kNormBwdRows;
+  const int nparts = static_cast<int>((static_cast<int64_t>(a->rows) + kNormBwdRows - 1) / kNormBwdRows);
   const float* x = static_cast<const float*>(a->x);
   const float* w = static_cast<const float*>(a->weight);
   switch (a->dy_dtype) {
@@ -380,10 +383,11 @@ extern "C" int32_t ssa_swiglu(const ssa_swiglu_args* a, void* stream) {
   if (a == nullptr || a->z == nullptr || a->out == nullptr || (a->backward && a->dh == nullptr))
     return SSA_OPS_ERR_NULL_POINTER;
   if (a->rows <= 0 || a->ffn <= 0 || a->ffn % 4 != 0) return SSA_OPS_ERR_SHAPE;
+  const int64_t threads = static_cast<int64_t>(a->rows) * (a->ffn / 4);  // one per 4 outputs
+  if ((threads + 255) / 256 > INT32_MAX) return SSA_OPS_ERR_SHAPE;
   if (a->dtype != 0 && a->dtype != 1) return SSA_OPS_ERR_DTYPE;
   if (!aligned(a->z, 8) || !aligned(a->out, 8) || (a->backward && !aligned(a->dh, 8))) return SSA_OPS_ERR_ALIGNMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t threads = static_cast<int64_t>(a->rows) * (a->ffn / 4);
   const int grid = static_cast<int>((threads + 255) / 256);
   if (a->dtype == 0)
     hipLaunchKernelGGL(swiglu_kernel<__bf16>, dim3(grid), dim3(256), 0, s, static_cast<const __bf16*>(a->z),

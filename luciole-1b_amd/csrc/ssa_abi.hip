@@ -25,11 +25,36 @@ int32_t check_tensor(const ssa_tensor4& t, bool required) {
   return SSA_OK;
 }
 
-int32_t check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t N, int32_t D, int32_t dtype) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0) return SSA_ERR_SHAPE;
-  if (Hq % Hkv != 0) return SSA_ERR_SHAPE;
-  // Grid sizes are int32 block counts; keep every product well inside range.
-  if (static_cast<int64_t>(B) * Hq * ((static_cast<int64_t>(N) + 127) / 128) > (1ll << 30)) return SSA_ERR_SHAPE;
+// Sizes every launcher can take with int32 arithmetic: sequence lengths up
+// to 2^30 (so N + tile - 1 fits), at most 2^28 units of 128 rows per grid
+// (the smallest workgroup covers 64 rows, so every grid size fits), and --
+// checked separately -- at most INT32_MAX query rows per launch over dense
+// batches (B * Hq * N) and packed streams (Hq * T), the rows the Delta kernels
+// cover.
+constexpr int64_t kMaxSeqlen = 1ll << 30;
+constexpr int64_t kMaxGridUnits = 1ll << 28;
+
+bool shape_ok(int32_t B, int32_t Hq, int32_t Hkv, int32_t N) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0 || N > kMaxSeqlen) return false;
+  if (Hq % Hkv != 0) return false;
+  const int64_t bh = static_cast<int64_t>(B) * Hq;
+  return bh <= kMaxGridUnits && bh * ((static_cast<int64_t>(N) + 127) / 128) <= kMaxGridUnits;
+}
+
+bool rows_ok(int64_t a, int64_t b, int64_t c) {
+  return a > 0 && b > 0 && c > 0 && a * b <= INT32_MAX && a * b * c <= INT32_MAX;
+}
+
+// a * b for non-negative operands, or -1 when either is negative or the
+// product does not fit int64.
+int64_t mul_or_neg(int64_t a, int64_t b) {
+  int64_t r = 0;
+  return (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r)) ? -1 : r;
+}
+
+int32_t check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t N, int32_t D, int32_t dtype, bool packed) {
+  if (!shape_ok(B, Hq, Hkv, N)) return SSA_ERR_SHAPE;
+  if (!packed && !rows_ok(B, Hq, N)) return SSA_ERR_SHAPE;
   if (dtype != SSA_DTYPE_BF16 && dtype != SSA_DTYPE_FP16 && dtype != SSA_DTYPE_FP32) return SSA_ERR_DTYPE;
   if (D != 32 && D != 64 && D != 128 && !(D == 16 && dtype == SSA_DTYPE_FP32)) return SSA_ERR_HEAD_DIM;
   return SSA_OK;
@@ -43,9 +68,9 @@ Tensor4 to_t4(const ssa_tensor4& t) { return Tensor4{t.ptr, t.stride_b, t.stride
     if (st_ != SSA_OK) return st_;    \
   } while (0)
 
-int32_t fill_fwd(const ssa_fwd_args* a, ssa::FwdParams* p) {
+int32_t fill_fwd(const ssa_fwd_args* a, ssa::FwdParams* p, bool packed) {
   if (a == nullptr) return SSA_ERR_NULL_POINTER;
-  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
+  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype, packed));
   SSA_TRY(check_tensor(a->q, true));
   SSA_TRY(check_tensor(a->k, true));
   SSA_TRY(check_tensor(a->v, true));
@@ -70,19 +95,21 @@ int32_t fill_fwd(const ssa_fwd_args* a, ssa::FwdParams* p) {
 
 // Packed batches: the document table itself lives on the device and is only
 // clamped there (see SeqView); the host checks what it can see.
-int32_t check_varlen(int32_t docs, int32_t max_seqlen, const int32_t* cu, int32_t total) {
+int32_t check_varlen(int32_t docs, int32_t heads_q, int32_t max_seqlen, const int32_t* cu, int32_t total) {
   if (cu == nullptr) return SSA_ERR_NULL_POINTER;
   if (total <= 0 || docs <= 0 || max_seqlen <= 0 || max_seqlen > total) return SSA_ERR_CU_SEQLENS;
+  if (!rows_ok(heads_q, total, 1)) return SSA_ERR_SHAPE;
   return SSA_OK;
 }
 
 int32_t launch_status(hipError_t e) { return e == hipSuccess ? SSA_OK : SSA_ERR_LAUNCH; }
 
 bool decode_shape_ok(int32_t B, int32_t Hq, int32_t Hkv, int32_t cap, int32_t requested) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || cap <= 0 || requested < 0 || Hq % Hkv != 0) return false;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || cap <= 0 || cap > kMaxSeqlen || requested < 0 || Hq % Hkv != 0) return false;
+  if (static_cast<int64_t>(B) * Hq >= (1ll << 30)) return false;
   // one workgroup per (batch, kv-head, group of 32 q-heads, split): int32 grid
-  const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31) / 32);
-  return units * ((static_cast<int64_t>(cap) + 127) / 128) < (1ll << 30) && static_cast<int64_t>(B) * Hq < (1ll << 30);
+  const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31ll) / 32);
+  return units * ((static_cast<int64_t>(cap) + 127) / 128) < (1ll << 30);
 }
 
 // Decode workspace: (m, l) pairs of every (batch, q-head, split) record,
@@ -101,9 +128,10 @@ namespace ssa {
 // Validation and parameters of the backward entry points.  with_workspaces =
 // false (ssa_bwd_noalloc) ignores delta, partials and ds_workspace: the
 // caller of that entry point supplies them from its own storage.
-int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces) {
+int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces,
+                        bool packed) {
   if (a == nullptr) return SSA_ERR_NULL_POINTER;
-  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype));
+  SSA_TRY(check_common(a->batch, a->heads_q, a->heads_kv, a->seqlen, a->head_dim, a->dtype, packed));
   SSA_TRY(check_tensor(a->out, true));
   SSA_TRY(check_tensor(a->dout, true));
   if (with_workspaces && a->delta == nullptr) return SSA_ERR_NULL_POINTER;
@@ -182,19 +210,27 @@ const char* ssa_status_string(int32_t status) {
 }
 
 int64_t ssa_bwd_partials_count(int32_t batch, int32_t heads_kv, int32_t seqlen) {
-  if (batch <= 0 || heads_kv <= 0 || seqlen <= 0) return 0;
+  if (!shape_ok(batch, heads_kv, heads_kv, seqlen)) return 0;
   return 2ll * batch * heads_kv * ssa::dkdv_key_blocks(seqlen);
 }
 
 int64_t ssa_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen, int32_t causal) {
-  if (batch <= 0 || heads_q <= 0 || seqlen <= 0) return 0;
-  return static_cast<int64_t>(batch) * heads_q * ssa::ds_tiles_per_head(seqlen, causal != 0) * 1024;
+  if (!shape_ok(batch, heads_q, heads_q, seqlen) || !rows_ok(batch, heads_q, seqlen)) return 0;
+  const int64_t tiles = mul_or_neg(static_cast<int64_t>(batch) * heads_q, ssa::ds_tiles_per_head(seqlen, causal != 0));
+  const int64_t bytes = mul_or_neg(tiles, 1024);
+  return bytes < 0 ? 0 : bytes;
 }
 
 int64_t ssa_varlen_bwd_ds_workspace_bytes(int32_t batch, int32_t heads_q, int32_t max_seqlen, int32_t total_tokens,
                                           int32_t causal) {
-  if (batch <= 0 || heads_q <= 0 || max_seqlen <= 0 || total_tokens < max_seqlen) return 0;
-  return ssa::ds_packed_tiles(batch, heads_q, total_tokens, max_seqlen, causal != 0) * 1024;
+  if (!shape_ok(batch, heads_q, heads_q, max_seqlen) || total_tokens < max_seqlen ||
+      !rows_ok(heads_q, total_tokens, 1))
+    return 0;
+  // ds_packed_tiles() = (T / 32 + B) * Hq * ds_slot_tiles(Nmax), multiplied with overflow checks
+  const int64_t slots = static_cast<int64_t>(total_tokens / 32) + batch;
+  const int64_t tiles = mul_or_neg(slots * heads_q, ssa::ds_slot_tiles(max_seqlen, causal != 0));
+  const int64_t bytes = mul_or_neg(tiles, 1024);
+  return bytes < 0 ? 0 : bytes;
 }
 
 int32_t ssa_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t capacity,
@@ -249,7 +285,7 @@ int32_t ssa_decode(const ssa_decode_args* a, void* stream) {
 
 int32_t ssa_fwd(const ssa_fwd_args* a, void* stream) {
   ssa::FwdParams p{};
-  SSA_TRY(fill_fwd(a, &p));
+  SSA_TRY(fill_fwd(a, &p, false));
   return launch_status(
       ssa::launch_fwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
@@ -258,8 +294,8 @@ int32_t ssa_varlen_fwd(const ssa_varlen_fwd_args* va, void* stream) {
   if (va == nullptr) return SSA_ERR_NULL_POINTER;
   const ssa_fwd_args* a = &va->dense;
   ssa::FwdParams p{};
-  SSA_TRY(fill_fwd(a, &p));
-  SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
+  SSA_TRY(fill_fwd(a, &p, true));
+  SSA_TRY(check_varlen(a->batch, a->heads_q, a->seqlen, va->cu_seqlens, va->total_tokens));
   p.cu_seqlens = va->cu_seqlens;
   p.T = va->total_tokens;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -283,8 +319,8 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   if (va == nullptr) return SSA_ERR_NULL_POINTER;
   const ssa_bwd_args* a = &va->dense;
   ssa::BwdParams p{};
-  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
-  SSA_TRY(check_varlen(a->batch, a->seqlen, va->cu_seqlens, va->total_tokens));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true, true));
+  SSA_TRY(check_varlen(a->batch, a->heads_q, a->seqlen, va->cu_seqlens, va->total_tokens));
   p.cu_seqlens = va->cu_seqlens;
   p.T = va->total_tokens;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -316,33 +352,33 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
 
 int32_t ssa_bwd_preprocess(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(ssa::fill_bwd_params(a, &p, true, true));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, true, true, false));
   return launch_status(ssa::launch_bwd_preprocess(p, a->dtype, a->head_dim, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_dkdv(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true, false));
   return launch_status(
       ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_dq(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true, false));
   return launch_status(
       ssa::launch_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd_reduce(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true, false));
   return launch_status(ssa::launch_reduce_partials(p, static_cast<hipStream_t>(stream)));
 }
 
 int32_t ssa_bwd(const ssa_bwd_args* a, void* stream) {
   ssa::BwdParams p{};
-  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true));
+  SSA_TRY(ssa::fill_bwd_params(a, &p, false, true, false));
   return ssa::run_bwd(p, a->dtype, a->head_dim, a->causal != 0, static_cast<hipStream_t>(stream));
 }
 

@@ -32,8 +32,11 @@ namespace ssa {
 
 // Backward entry points (ssa_abi.hip): validation + parameters, and the four
 // launches of a whole backward in order.  with_workspaces = false leaves
-// delta, partials and ds unset for a caller that supplies them itself.
-int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces);
+// delta, partials and ds unset for a caller that supplies them itself;
+// packed = true skips the dense row-count limit (a packed stream's rows are
+// checked against its token count instead).
+int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces,
+                        bool packed);
 int32_t run_bwd(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s);
 
 // Packed batches: write the token rows no document covers (ssa_varlen_fill.hip):
@@ -56,20 +59,20 @@ hipError_t launch_varlen_fill(const VarlenFill& f, hipStream_t stream);
 // round of workgroups costs more than the longer splits save) but no split
 // shorter than 256 keys.
 inline int decode_split_keys(int cap, int splits) {
-  const int sk = (cap + splits - 1) / splits;
-  return (sk + 127) / 128 * 128;
+  const int64_t sk = (static_cast<int64_t>(cap) + splits - 1) / splits;
+  return static_cast<int>((sk + 127) / 128 * 128);
 }
 inline int decode_splits(int B, int Hq, int Hkv, int cap, int requested) {
   int want = requested;
   if (want <= 0) {
-    const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31) / 32);
-    const int64_t most = (cap + 255) / 256;
+    const int64_t units = static_cast<int64_t>(B) * Hkv * ((Hq / Hkv + 31ll) / 32);
+    const int64_t most = (cap + 255ll) / 256;
     const int64_t w = (256 + units - 1) / units;
     want = static_cast<int>(w < most ? w : most);
     if (want < 1) want = 1;
   }
-  const int sk = decode_split_keys(cap, want);
-  return (cap + sk - 1) / sk;
+  const int64_t sk = decode_split_keys(cap, want);
+  return static_cast<int>((cap + sk - 1) / sk);
 }
 
 // Number of key blocks of the dK/dV kernel (each writes one dn and one db partial).

@@ -52,7 +52,7 @@ extern "C" int32_t ssa_bwd_noalloc(const ssa_bwd_args* a, void* stream) {
   // Validated like ssa_bwd; the caller's delta, partials and ds_workspace
   // fields are ignored.
   ssa::BwdParams p{};
-  const int32_t st = ssa::fill_bwd_params(a, &p, false, false);
+  const int32_t st = ssa::fill_bwd_params(a, &p, false, false, false);
   if (st != SSA_OK) return st;
   const int64_t delta_bytes = round256(static_cast<int64_t>(a->batch) * a->heads_q * a->seqlen * 4);
   const int64_t part_bytes = 2ll * a->batch * a->heads_kv * ssa::dkdv_key_blocks(a->seqlen) * 4;

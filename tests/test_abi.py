@@ -160,6 +160,26 @@ def test_fp32_head_dims():
         assert _lib.lib().ssa_bwd(ctypes.byref(b), None) == _lib.SSA_ERR_HEAD_DIM, D
 
 
+def test_size_limits():
+    """Shapes whose grid or row arithmetic would leave int32 are refused before any launch:
+    seqlen > 2^30, more than INT32_MAX dense query rows, huge decode caches; the size
+    queries return 0 for them instead of an overflowed value."""
+    lib = _lib.lib()
+    for over in ({"seqlen": (1 << 30) + 1}, {"batch": 1 << 16, "heads_q": 1 << 10, "heads_kv": 1 << 10},
+                 {"seqlen": 2**31 - 1}):
+        a = _fwd_args(**over)
+        assert lib.ssa_fwd(ctypes.byref(a), None) == _lib.SSA_ERR_SHAPE, over
+        b = _bwd_args(**over)
+        assert lib.ssa_bwd(ctypes.byref(b), None) == _lib.SSA_ERR_SHAPE, over
+    assert lib.ssa_bwd_ds_workspace_bytes(1 << 16, 1 << 10, 4096, 1) == 0
+    assert lib.ssa_bwd_ds_workspace_bytes(2**31 - 1, 2**31 - 1, 2**31 - 1, 1) == 0
+    assert lib.ssa_bwd_partials_count(2**31 - 1, 2**31 - 1, 1 << 30) == 0
+    assert lib.ssa_varlen_bwd_ds_workspace_bytes(2**31 - 1, 2**31 - 1, 1 << 30, 2**31 - 1, 1) == 0
+    assert lib.ssa_decode_num_splits(1, 8, 8, 2**31 - 1, 0) == 0
+    assert lib.ssa_decode_num_splits(1, 8, 8, 4096, 2**31 - 1) == 32  # more splits than 128-key blocks: clamped
+    assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 4096, 1) == 4 * 16 * 128 * 129 * 1024
+
+
 def test_fwd_null_args():
     assert _lib.lib().ssa_fwd(None, None) == _lib.SSA_ERR_NULL_POINTER
 

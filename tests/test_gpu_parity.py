@@ -101,6 +101,25 @@ def test_parity_fp32_trained_n(gpu):
     _check(*_run(gpu, 1, 4, 4, 300, 128, torch.float32, False, n_val=4.0, qkv_scale=0.5))
 
 
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["contig", "strided"])
+def test_delta_direct(gpu, D, dtype, layout):
+    """Delta = rowsum(dO * O) (ssa_triton_kernel.py:267-298) from ssa_bwd_preprocess against
+    the fp64 row sums of the same (rounded) values: fp32 accumulation over D terms, so
+    |err| <= 1e-5 * sum_d |o_d dO_d| + 1e-7."""
+    from SSA.ssa_hip_kernel import ssa_bwd_preprocess
+
+    print(f"[gpu case] delta D={D} {dtype} {layout}", file=sys.stderr, flush=True)
+    o, _, _, do = make_inputs(2, 3, 3, 300, D, dtype, gpu, layout, seed=99)
+    delta = ssa_bwd_preprocess(o, do)
+    torch.cuda.synchronize()
+    od = o.double().cpu() * do.double().cpu()
+    ref, mag = od.sum(-1), od.abs().sum(-1)
+    err = (delta.double().cpu() - ref).abs()
+    assert delta.shape == (2, 3, 300) and bool((err <= 1e-5 * mag + 1e-7).all()), float((err / (mag + 1e-12)).max())
+
+
 @pytest.mark.parametrize("D", [8, 256])
 def test_unsupported_head_dims_raise(gpu, D):
     from SSA.ssa_triton_kernel import ssa_flash_attn_forward
