@@ -21,13 +21,13 @@ device (no host synchronisation); ``dn`` / ``db`` come back as 0-d fp32 tensors.
 
 Differences from the reference, all widening: any sequence length (the
 reference's backward needs N % 128 == 0), and results are bitwise
-reproducible.  For head dim 128 the backward by default keeps dS' (the score
+reproducible.  In bf16 / fp16 the backward by default keeps dS' (the score
 gradient, input dtype, causal triangle only: 2 N^2 bytes per (batch, head)) in
 a transient workspace so that dQ is one streaming product with K instead of
-the reference's recompute of the scores (measured faster at D = 128, slower at
-D = 64, where the recompute is cheap); ``SSA_BWD_DS=0`` / ``1`` forces either
-path, and a workspace above ``SSA_BWD_DS_MAX_BYTES`` (default 16 GiB) always
-recomputes.  Head dims 32, 64 and 128 run on kernels of their own; in bf16 /
+the reference's recompute of the scores (measured faster at every head dim:
+3-6 % of the backward at D = 32 / 64, 7-17 % at D = 128); ``SSA_BWD_DS=0`` /
+``1`` forces either path, and a workspace above ``SSA_BWD_DS_MAX_BYTES``
+(default 16 GiB) always recomputes.  Head dims 32, 64 and 128 run on kernels of their own; in bf16 /
 fp16, head dim 16 (the smallest the reference's Triton kernel takes) runs on
 the D = 32 kernels with its operands zero-padded to 32 columns, which changes
 no score, dP or Delta, and the results are sliced back (the decode step is not
@@ -142,8 +142,9 @@ def ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True):
 
 def _use_ds_workspace(nbytes: int, head_dim: int, ds) -> bool:
     """Whether the backward keeps dS' in a workspace of ``nbytes`` bytes
-    (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy: on for
-    head dim 128 within ``SSA_BWD_DS_MAX_BYTES``)."""
+    (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy: on
+    within ``SSA_BWD_DS_MAX_BYTES``).  ``head_dim`` is kept for callers; every
+    head dim measured faster with the workspace."""
     if ds is not None:
         return bool(ds)
     mode = os.environ.get("SSA_BWD_DS", "auto").strip().lower()
@@ -152,7 +153,7 @@ def _use_ds_workspace(nbytes: int, head_dim: int, ds) -> bool:
     if mode in ("1", "on", "true", "yes"):
         return True
     limit = int(os.environ.get("SSA_BWD_DS_MAX_BYTES", str(16 << 30)))
-    return head_dim == 128 and nbytes <= limit
+    return 0 < nbytes <= limit
 
 
 class BackwardLaunch:

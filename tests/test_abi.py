@@ -459,3 +459,22 @@ def test_built_device_assembly_has_no_short_waits():
     if not asms:
         pytest.skip("no device assembly: run build() first")
     assert _hazards.check_files(asms) == []
+
+
+def test_ds_workspace_policy(monkeypatch):
+    """The Python layer's dS' workspace policy: on for every head dim within
+    SSA_BWD_DS_MAX_BYTES, forced either way by SSA_BWD_DS or the ds argument."""
+    from SSA.ssa_hip_kernel import _use_ds_workspace
+
+    monkeypatch.delenv("SSA_BWD_DS", raising=False)
+    monkeypatch.delenv("SSA_BWD_DS_MAX_BYTES", raising=False)
+    for D in (32, 64, 128):
+        assert _use_ds_workspace(1 << 30, D, None)
+        assert not _use_ds_workspace(17 << 30, D, None)     # above the 16 GiB default cap
+        assert not _use_ds_workspace(1 << 20, D, False) and _use_ds_workspace(17 << 30, D, True)
+    monkeypatch.setenv("SSA_BWD_DS_MAX_BYTES", str(1 << 20))
+    assert not _use_ds_workspace(1 << 21, 64, None) and _use_ds_workspace(1 << 20, 64, None)
+    monkeypatch.setenv("SSA_BWD_DS", "0")
+    assert not _use_ds_workspace(1 << 10, 128, None)
+    monkeypatch.setenv("SSA_BWD_DS", "1")
+    assert _use_ds_workspace(1 << 40, 32, None)
