@@ -1018,11 +1018,13 @@ static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// dS' K pass: 8 waves (256 queries, one 128 KB workgroup per CU) at head
-// dim 128, so each K tile is read once per 256 queries; 4 waves otherwise.
+// dS' K pass: 8 waves (256 queries per workgroup; 128 KB of LDS at head dim
+// 128, 112 KB at 64) at head dims 64 and 128, so each K tile is read once per
+// 256 queries (measured 4 % faster than 4-wave workgroups at both); 4 waves
+// at head dim 32.
 template <int D>
 constexpr int dq_ds_waves() {
-  return D == 128 ? 8 : 4;
+  return D >= 64 ? 8 : 4;
 }
 
 template <typename T, int D, bool CAUSAL>

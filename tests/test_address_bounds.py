@@ -233,7 +233,7 @@ def check_dq_ds(B, Hq, Hkv, Nmax, D, causal, k_st, written, cu=None, T=0):
     """The dS' K pass: K tile loads (row-swizzled at D = 128) and the dS' tile
     loads of every wave; every dS' byte read was written by dK/dV unless the
     kernel multiplies it by zero (tiles past the wave's last one)."""
-    NW = 8 if D == 128 else 4
+    NW = 8 if D >= 64 else 4
     BM, BN = 32 * NW, 64
     sb, sh, ss = k_st
     packed = cu is not None
