@@ -1,8 +1,9 @@
 """ssa_bwd_noalloc: the backward that allocates nothing (Delta and the dn/db
 partials in the library's static device scratch, dQ recomputed).
 
-Called through the C ABI on two problems in a row -- the second smaller, so
-it runs on the scratch the first left behind -- and compared with ssa_bwd on
+Called through the C ABI on three problems in a row -- each smaller, so each
+runs on the scratch the previous one left behind, the last on the fp32
+kernels -- and compared with ssa_bwd on
 the same arguments (recompute path, caller workspaces): bitwise equal, and
 within the parity bar of the fp64 oracle (tests/parity_util.py).  The
 caller's delta / partials fields are NULL, so nothing of the caller's is used
@@ -22,9 +23,11 @@ from parity_util import assert_parity, compare, make_inputs, oracle_fwd_bwd, sca
 pytestmark = pytest.mark.gpu
 
 CALLS = [
-    # B, Hq, Hkv, N, D, causal: larger first, then smaller
-    (2, 8, 4, 700, 128, True),
-    (1, 4, 2, 200, 64, False),
+    # B, Hq, Hkv, N, D, causal, dtype: larger first, then smaller (the last on
+    # the fp32 kernels, to the fp32 bars)
+    (2, 8, 4, 700, 128, True, torch.bfloat16),
+    (1, 4, 2, 200, 64, False, torch.bfloat16),
+    (1, 4, 4, 150, 16, True, torch.float32),
 ]
 
 
@@ -33,10 +36,10 @@ def test_noalloc_equals_ssa_bwd_on_two_calls(gpu):
     from SSA.ssa_hip_kernel import BackwardLaunch, ssa_flash_attn_forward
 
     lib = _lib.lib()
-    for i, (B, Hq, Hkv, N, D, causal) in enumerate(CALLS):
-        label = f"noalloc call {i}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={int(causal)}"
+    for i, (B, Hq, Hkv, N, D, causal, dtype) in enumerate(CALLS):
+        label = f"noalloc call {i}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={int(causal)} {dtype}"
         print(f"[gpu case] {label}", file=sys.stderr, flush=True)
-        q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, gpu, "contig", 1234 + i, 0.5)
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, gpu, "contig", 1234 + i, 0.5)
         n = torch.tensor(1.5, device=gpu)
         b = torch.tensor(0.8, device=gpu)
         scale = scale_for(D)
