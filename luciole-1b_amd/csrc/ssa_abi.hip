@@ -174,12 +174,21 @@ int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_onl
   return SSA_OK;
 }
 
+// dQ then the dn / db reduction: on the workspace path (bf16 / fp16 with a
+// dS' workspace) the dQ pass's first workgroup does the reduction, so it
+// needs no launch of its own.
+int32_t run_dq_and_reduce(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s) {
+  BwdParams pq = p;
+  pq.fuse_reduce = p.ds != nullptr && dtype != SSA_DTYPE_FP32;
+  SSA_TRY(launch_status(launch_bwd_dq(pq, dtype, D, causal, s)));
+  return pq.fuse_reduce ? SSA_OK : launch_status(launch_reduce_partials(p, s));
+}
+
 // The whole backward on one stream: preprocess, dK/dV, dQ, reduction.
 int32_t run_bwd(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s) {
   SSA_TRY(launch_status(launch_bwd_preprocess(p, dtype, D, s)));
   SSA_TRY(launch_status(launch_bwd_dkdv(p, dtype, D, causal, s)));
-  SSA_TRY(launch_status(launch_bwd_dq(p, dtype, D, causal, s)));
-  return launch_status(launch_reduce_partials(p, s));
+  return run_dq_and_reduce(p, dtype, D, causal, s);
 }
 
 }  // namespace ssa
@@ -332,8 +341,7 @@ int32_t ssa_varlen_bwd(const ssa_varlen_bwd_args* va, void* stream) {
   pre.N = va->total_tokens;
   SSA_TRY(launch_status(ssa::launch_bwd_preprocess(pre, a->dtype, a->head_dim, s)));
   SSA_TRY(launch_status(ssa::launch_bwd_dkdv(p, a->dtype, a->head_dim, causal, s)));
-  SSA_TRY(launch_status(ssa::launch_bwd_dq(p, a->dtype, a->head_dim, causal, s)));
-  SSA_TRY(launch_status(ssa::launch_reduce_partials(p, s)));
+  SSA_TRY(ssa::run_dq_and_reduce(p, a->dtype, a->head_dim, causal, s));
   ssa::VarlenFill f{};
   f.t[0] = p.dq;
   f.t[1] = p.dk;

@@ -781,21 +781,23 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dn, db = fixed-order sums of the per-workgroup partials (one workgroup).
-__global__ __launch_bounds__(256) void ssa_reduce_partials_kernel(const float* partials, int64_t count,
-                                                                  float* dn, float* db) {
-  __shared__ float sh[2][256];
-  const int tid = threadIdx.x;
+// dn, db = fixed-order sums of the per-workgroup partials: threads 0 .. 255
+// of the calling workgroup Kahan-sum strided slices, then a fixed tree; every
+// thread of the workgroup reaches the barriers.
+__device__ __forceinline__ void reduce_partials_body(const float* partials, int64_t count, float* dn, float* db,
+                                                     float (*sh)[256], int tid) {
+  if (tid < 256) {
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const float* src = partials + w * count;
-    float acc = 0.f, comp = 0.f;
-    for (int64_t i = tid; i < count; i += 256) {
-      const float y = src[i] - comp, t = acc + y;
-      comp = (t - acc) - y;
-      acc = t;
+    for (int w = 0; w < 2; ++w) {
+      const float* src = partials + w * count;
+      float acc = 0.f, comp = 0.f;
+      for (int64_t i = tid; i < count; i += 256) {
+        const float y = src[i] - comp, t = acc + y;
+        comp = (t - acc) - y;
+        acc = t;
+      }
+      sh[w][tid] = acc;
     }
-    sh[w][tid] = acc;
   }
   __syncthreads();
   for (int stride = 128; stride > 0; stride >>= 1) {
@@ -809,6 +811,13 @@ __global__ __launch_bounds__(256) void ssa_reduce_partials_kernel(const float* p
     *dn = sh[0][0];
     *db = sh[1][0];
   }
+}
+
+// The reduction as a launch of its own (one workgroup).
+__global__ __launch_bounds__(256) void ssa_reduce_partials_kernel(const float* partials, int64_t count,
+                                                                  float* dn, float* db) {
+  __shared__ float sh[2][256];
+  reduce_partials_body(partials, count, dn, db, sh, threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -839,7 +848,16 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   constexpr int KP = (BN / 32) * BL::IPB / NW;  // K load pieces per wave and tile
   static_assert(KP >= 1, "K tile split");
   static_assert(PFD > PFK && PFK >= 1 && PFK < NK && PFD < NDS, "ring depths");
+  static_assert(NW * 64 >= 256, "the fused reduction needs 256 threads");
   __shared__ __attribute__((aligned(1024))) char smem[NK * KTILE + NDS * DSTAGE];
+  __shared__ float red_sh[2][256];
+
+  // The backward's dn / db reduction, before this workgroup issues any load
+  // (the partials are complete: dK/dV ran before this kernel).
+  if (p.fuse_reduce && blockIdx.x == 0) {
+    const int64_t count = static_cast<int64_t>(p.B) * p.Hkv * dkdv_key_blocks(p.N);
+    reduce_partials_body(p.partials, count, p.dn, p.db, red_sh, threadIdx.x);
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

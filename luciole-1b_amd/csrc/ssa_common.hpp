@@ -146,6 +146,10 @@ struct BwdParams {
   // Optional dS' workspace (dense batches): when set, dK/dV writes the
   // gradient tiles there and dQ is a product with K instead of a recompute.
   void* ds;
+  // Workspace dQ pass only: its workgroup 0 also sums the dn / db partials
+  // (the reduction of ssa_reduce_partials_kernel, bit for bit), so the whole
+  // backward needs no separate reduction launch.
+  int fuse_reduce;
 };
 
 // Decode against a KV cache: q / o [B, Hq, 1, D] (row stride unused), k / v

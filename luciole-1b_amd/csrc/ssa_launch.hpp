@@ -38,6 +38,7 @@ namespace ssa {
 int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_only, bool with_workspaces,
                         bool packed);
 int32_t run_bwd(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s);
+int32_t run_dq_and_reduce(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s);
 
 // Packed batches: write the token rows no document covers (ssa_varlen_fill.hip):
 // up to three [T, H, D] tensors of esize-byte elements (rows set to 0) and

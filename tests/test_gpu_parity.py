@@ -187,6 +187,32 @@ def test_determinism_bitwise(gpu):
             assert torch.equal(a, c), f"non-deterministic result ({layout})"
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("ds", [True, False], ids=["ds", "recompute"])
+def test_whole_backward_equals_its_stages_bitwise(gpu, D, ds):
+    """ssa_bwd (on the workspace path the dQ pass also sums dn / db) against the
+    four staged entry points, ssa_bwd_preprocess / _dkdv / _dq / _reduce, on the
+    same arguments: every output bit for bit."""
+    from SSA.ssa_hip_kernel import BackwardLaunch, ssa_flash_attn_forward
+
+    print(f"[gpu case] whole vs staged backward D={D} ds={ds}", file=sys.stderr, flush=True)
+    q, k, v, do = make_inputs(2, 8, 2, 700, D, torch.bfloat16, gpu, "contig", 77, 0.5)
+    n = torch.tensor(1.5, device=gpu)
+    b = torch.tensor(0.8, device=gpu)
+    out, m = ssa_flash_attn_forward(q, k, v, scale_for(D), n, b, True)
+    whole = BackwardLaunch(q, k, v, out, do, m, scale_for(D), n, b, True, ds=ds)
+    staged = BackwardLaunch(q, k, v, out, do, m, scale_for(D), n, b, True, ds=ds)
+    for t in whole.results() + staged.results():
+        t.fill_(float("nan"))
+    whole.run()
+    for stage in BackwardLaunch.STAGES:
+        staged.run_stage(stage)
+    torch.cuda.synchronize()
+    for name, a, c in zip(("dq", "dk", "dv", "dn", "db"), whole.results(), staged.results()):
+        assert torch.equal(a, c), f"D={D} ds={ds}: {name} of ssa_bwd differs from the staged backward"
+    assert torch.isfinite(whole.dn) and torch.isfinite(whole.db)
+
+
 @pytest.mark.parametrize("ds", [True, False], ids=["ds", "recompute"])
 def test_dkdv_wide_row_range_bitwise(gpu, ds):
     """dK/dV addresses a workgroup's Q / dO rows with 32-bit offsets when they
