@@ -45,6 +45,7 @@ for _p in (str(ROOT), str(ROOT / "luciole-1b_amd")):
 # MI355X published dense peaks.
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (2.5 PFLOP/s class)
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP32_TFLOPS = 157.3   # MI355X fp32, vector ALU and dense matrix alike
 
 CONFIGS = {
     # name: (B, Hq, Hkv, S, D, causal)
@@ -338,7 +339,8 @@ def main():
                     choices=sorted(CONFIGS) + sorted(VARLEN_CONFIGS) + sorted(DECODE_CONFIGS) + sorted(TRAIN_CONFIGS))
     ap.add_argument("--kernel-iters", type=int, default=50, help="launches per kernel for per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16", "fp32"],
+                    help="fp32 (dense shapes only): the fp32 vector-ALU kernels, against the fp32 peak")
     ap.add_argument("--counters-summary", nargs="+", metavar="DB",
                     help="print the per-kernel counter table of rocprofv3 --pmc databases of --pmc-pass runs "
                          "(the table of profiles/ssa_counters_<config>.md) and exit")
@@ -365,6 +367,9 @@ def main():
     if args.warmup is None:
         args.warmup = 2 if train else 50
 
+    if args.dtype == "fp32" and args.config not in CONFIGS:
+        print(json.dumps({"error": "--dtype fp32 applies to the dense configs only (" + ", ".join(sorted(CONFIGS)) + ")"}))
+        sys.exit(2)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the SSA op has no cross-GPU "
@@ -386,7 +391,7 @@ def main():
     if args.config in TRAIN_CONFIGS:
         return bench_train(args, dev)
     B, Hq, Hkv, S, D, causal = CONFIGS[args.config]
-    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[args.dtype]
     torch.manual_seed(1234)
     q = (torch.randn(B, Hq, S, D, device=dev) * 0.5).to(dtype)
     k = (torch.randn(B, Hkv, S, D, device=dev) * 0.5).to(dtype)
@@ -459,16 +464,18 @@ def main():
     ds_bytes = launch.ds.numel() if launch.ds is not None else 0
     kernels["ssa_bwd_dkdv_kernel"]["alg_flop"] = 8 * D * pairs
     kernels["ssa_bwd_dq_kernel"]["alg_flop"] = 2 * D * pairs
-    esize = 2
+    esize = 4 if dtype == torch.float32 else 2
     if ds_bytes:
         kernels["ssa_bwd_dq_kernel"]["alg_bytes"] = ds_bytes + (B * Hkv + B * Hq) * S * D * esize
     pre_bytes = 2 * B * Hq * S * D * esize + 4 * B * Hq * S
     kernels["ssa_bwd_preprocess_kernel"]["alg_bytes"] = pre_bytes
+    # fp32 runs on the vector ALU (MI355X fp32: 157.3 TFLOP/s, vector and matrix alike)
+    peak_flops = PEAK_FP32_TFLOPS if dtype == torch.float32 else PEAK_BF16_TFLOPS
     for name, kd in kernels.items():
         if "alg_flop" in kd:
             kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
-            kd["frac_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
-            kd["bound"] = "mfma"
+            kd["frac_peak"] = kd["tflops"] / peak_flops
+            kd["bound"] = "valu" if dtype == torch.float32 else "mfma"
         if "alg_bytes" in kd:
             kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
             kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
@@ -482,9 +489,9 @@ def main():
         kd["counters"] = counters.get(hip_name.get(name, name))
     dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
     kd = kernels[dominant]
-    if kd.get("bound") == "mfma":
-        roofline = {"kernel": dominant, "bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": kd["tflops"] / PEAK_BF16_TFLOPS, "traffic": kd["hbm_bytes"],
+    if kd.get("bound") in ("mfma", "valu"):
+        roofline = {"kernel": dominant, "bound": kd["bound"], "achieved": kd["tflops"], "peak": peak_flops,
+                    "unit": "TFLOP/s", "frac": kd["tflops"] / peak_flops, "traffic": kd["hbm_bytes"],
                     "avg_launch_ms": kd["avg_ms"]}
         cn = kd.get("counters")
         if cn:

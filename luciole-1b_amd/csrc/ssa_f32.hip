@@ -7,12 +7,14 @@
 // (check_ssa_triton_parity.py:1064-1069), a bar that no bf16 rounding of the
 // operands meets.  These kernels keep every product in fp32 FMA and every
 // transcendental in the hardware's f32 exp2 / log2 / rcp.  They follow the
-// equations of ssa_fwd.hip / ssa_bwd.hip with simple structures (one or two
-// lanes per row, the other operand's rows shared through LDS and read as
-// broadcasts); the bf16 / fp16 kernels are the fast path, these the
-// full-precision one.  Masks, GQA, packed sequences and the dn / db partials
-// (one per 128-key block, the layout ssa_reduce_partials_kernel sums) are
-// those of the bf16 / fp16 path.
+// equations of ssa_fwd.hip / ssa_bwd.hip with simple structures: each row of
+// the register-resident operand is split over P adjacent lanes (P = D / 32 at
+// head dims 64 and 128, so a lane holds at most 32 columns of each row; the
+// partial dot products meet by butterfly shuffles), and the other operand's
+// rows are shared through LDS and read as broadcasts.  The bf16 / fp16
+// kernels are the fast path, these the full-precision one.  Masks, GQA,
+// packed sequences and the dn / db partials (one per 128-key block, the
+// layout ssa_reduce_partials_kernel sums) are those of the bf16 / fp16 path.
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
 
@@ -28,18 +30,62 @@ __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4
 // sL = sign(x) log2(1 + c|x|) for a raw score x = q.k, c = scale b; u1 = 1 + c|x|
 __device__ __forceinline__ float ssa_sl(float x, float u1) { return copysignf(fast_log2(u1), x); }
 
-constexpr int kF32Rows = 64;   // query rows per forward workgroup (one wave, one row per lane)
+constexpr int kF32Rows = 64;   // query rows per forward workgroup
 constexpr int kF32Tile = 32;   // rows per LDS tile of the streamed operand
-constexpr int kF32Pair = 128;  // rows per backward workgroup (two lanes per row, 256 threads)
+constexpr int kF32Pair = 128;  // keys (dK/dV) or queries (dQ) per backward workgroup
+
+// Lanes per row: the forward splits rows from head dim 64 on, the backward
+// (which holds two or three row operands per lane) always.
+template <int D>
+constexpr int fwd_parts() {
+  return D >= 64 ? D / 32 : 1;
+}
+template <int D>
+constexpr int bwd_parts() {
+  return D >= 64 ? D / 32 : 2;
+}
+template <int D>
+constexpr int fwd_threads() {
+  return kF32Rows * fwd_parts<D>();
+}
+template <int D>
+constexpr int bwd_threads() {
+  return kF32Pair * bwd_parts<D>();
+}
+
+// Dot product of a lane's CP four-column chunks with the same chunks of an
+// LDS row.
+template <int CP>
+__device__ __forceinline__ float part_dot(const f32x4* reg, const f32x4* lds) {
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CP; ++c) {
+    const f32x4 x = lds[c];
+    s = fmaf(reg[c].x, x.x, s);
+    s = fmaf(reg[c].y, x.y, s);
+    s = fmaf(reg[c].z, x.z, s);
+    s = fmaf(reg[c].w, x.w, s);
+  }
+  return s;
+}
+
+// Sum over the P adjacent lanes of a row (P in {1, 2, 4}); every lane gets it.
+template <int P>
+__device__ __forceinline__ float sum_parts(float x) {
+  if constexpr (P >= 2) x += __shfl_xor(x, 1, 64);
+  if constexpr (P >= 4) x += __shfl_xor(x, 2, 64);
+  return x;
+}
 
 // ---------------------------------------------------------------------------
-// Forward: lane = one query row, q and the accumulator in registers, K / V
-// tiles of 32 keys in LDS; exact running max (online softmax in base 2).
+// Forward: P lanes = one query row, the lane's share of q and of the
+// accumulator in registers, K / V tiles of 32 keys in LDS; exact running max
+// (online softmax in base 2), the same in the P lanes of a row.
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(64) void ssa_fwd_f32_kernel(FwdParams p) {
-  constexpr int C4 = D / 4;
+__global__ __launch_bounds__(fwd_threads<D>()) void ssa_fwd_f32_kernel(FwdParams p) {
+  constexpr int P = fwd_parts<D>(), C4 = D / 4, CP = C4 / P, NT = fwd_threads<D>();
   __shared__ f32x4 ks[kF32Tile * C4], vs[kF32Tile * C4];
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, part = tid % P;
   const int nqb = (p.N + kF32Rows - 1) / kF32Rows;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh % p.B, h = bh / p.B, hk = h / (p.Hq / p.Hkv);
@@ -47,24 +93,24 @@ __global__ __launch_bounds__(64) void ssa_fwd_f32_kernel(FwdParams p) {
   const int N = sv.N;
   const int q0 = qb * kF32Rows;
   if (q0 >= N) return;  // packed: past the end of a shorter document
-  const int i = q0 + lane;
+  const int i = q0 + tid / P;
   const float* qg = static_cast<const float*>(p.q.ptr) + sv.off(p.q, b) + h * p.q.sh;
   const float* kg = static_cast<const float*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
   const float* vg = static_cast<const float*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
   float* og = static_cast<float*>(const_cast<void*>(p.o.ptr)) + sv.off(p.o, b) + h * p.o.sh;
   const float n = *p.n_ptr, c = p.scale * *p.b_ptr;
 
-  f32x4 qv[C4], acc[C4];
+  f32x4 qv[CP], acc[CP];
 #pragma unroll
-  for (int c4 = 0; c4 < C4; ++c4) {
-    qv[c4] = i < N ? ld4(qg + i * p.q.ss + 4 * c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c4 = 0; c4 < CP; ++c4) {
+    qv[c4] = i < N ? ld4(qg + i * p.q.ss + 4 * (part * CP + c4)) : f32x4{0.f, 0.f, 0.f, 0.f};
     acc[c4] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float m = -__builtin_inff(), l = 0.f;
   const int kv_end = CAUSAL ? min(N, q0 + kF32Rows) : N;
   for (int k0 = 0; k0 < kv_end; k0 += kF32Tile) {
     __syncthreads();  // the previous tile is consumed
-    for (int idx = lane; idx < kF32Tile * C4; idx += kF32Rows) {
+    for (int idx = tid; idx < kF32Tile * C4; idx += NT) {
       const int row = min(k0 + idx / C4, N - 1), c4 = idx % C4;
       ks[idx] = ld4(kg + row * p.k.ss + 4 * c4);
       vs[idx] = ld4(vg + row * p.v.ss + 4 * c4);
@@ -72,36 +118,29 @@ __global__ __launch_bounds__(64) void ssa_fwd_f32_kernel(FwdParams p) {
     __syncthreads();
     const int kn = min(kF32Tile, kv_end - k0);
     for (int j = 0; j < kn; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int c4 = 0; c4 < C4; ++c4) {
-        const f32x4 kk = ks[j * C4 + c4];
-        s = fmaf(qv[c4].x, kk.x, s);
-        s = fmaf(qv[c4].y, kk.y, s);
-        s = fmaf(qv[c4].z, kk.z, s);
-        s = fmaf(qv[c4].w, kk.w, s);
-      }
+      const float s = sum_parts<P>(part_dot<CP>(qv, ks + j * C4 + part * CP));
       if (i < N && (!CAUSAL || k0 + j <= i)) {
         const float t2 = n * ssa_sl(s, fmaf(c, fabsf(s), 1.f));
         if (t2 > m) {  // the running max moves: rescale what is summed so far
           const float alpha = fast_exp2(m - t2);
           l *= alpha;
 #pragma unroll
-          for (int c4 = 0; c4 < C4; ++c4) acc[c4] *= alpha;
+          for (int c4 = 0; c4 < CP; ++c4) acc[c4] *= alpha;
           m = t2;
         }
         const float pv = fast_exp2(t2 - m);
         l += pv;
+        const f32x4* vrow = vs + j * C4 + part * CP;
 #pragma unroll
-        for (int c4 = 0; c4 < C4; ++c4) acc[c4] += pv * vs[j * C4 + c4];
+        for (int c4 = 0; c4 < CP; ++c4) acc[c4] += pv * vrow[c4];
       }
     }
   }
   if (i < N) {
     const float inv = 1.f / l;  // every row has a key (causal: itself)
 #pragma unroll
-    for (int c4 = 0; c4 < C4; ++c4) st4(og + i * p.o.ss + 4 * c4, acc[c4] * inv);
-    p.m[sv.mrow(b, h, p.Hq, p.T, p.N) + i] = m + log2f(l);
+    for (int c4 = 0; c4 < CP; ++c4) st4(og + i * p.o.ss + 4 * (part * CP + c4), acc[c4] * inv);
+    if (part == 0) p.m[sv.mrow(b, h, p.Hq, p.T, p.N) + i] = m + log2f(l);
   }
 }
 
@@ -127,63 +166,47 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_f32_kernel(BwdParams p
   if (row < total && sub == 0) p.delta[row] = acc;
 }
 
-// Dot product of a lane's half row (D / 2 columns in registers) with the same
-// half of an LDS row; the two lanes of a row add their halves.
-template <int H4>
-__device__ __forceinline__ float half_dot(const f32x4* reg, const f32x4* lds) {
-  float s = 0.f;
-#pragma unroll
-  for (int c4 = 0; c4 < H4; ++c4) {
-    const f32x4 x = lds[c4];
-    s = fmaf(reg[c4].x, x.x, s);
-    s = fmaf(reg[c4].y, x.y, s);
-    s = fmaf(reg[c4].z, x.z, s);
-    s = fmaf(reg[c4].w, x.w, s);
-  }
-  return s;
-}
-
 // ---------------------------------------------------------------------------
-// dK, dV (+ dn / db partials) for 128 keys of one (batch, kv-head): two lanes
-// per key, each holding half of k, v, dK, dV; Q / dO tiles of 32 rows, with M
-// and Delta, in LDS, over every q-head of the GQA group.  Per valid pair, as in
-// ssa_bwd.hip: P = exp2(n sL - M), dT = P (dP - Delta), dS' = dT / (1 + c|x|),
-// dV += P dO, dK += dS' q (scaled by scale n b at the end), dn += ln2 dT sL,
-// db += n scale dS' x.
+// dK, dV (+ dn / db partials) for 128 keys of one (batch, kv-head): P lanes
+// per key, each holding its share of k, v, dK, dV; Q / dO tiles of 32 rows,
+// with M and Delta, in LDS, over every q-head of the GQA group.  Per valid
+// pair, as in ssa_bwd.hip: P = exp2(n sL - M), dT = P (dP - Delta),
+// dS' = dT / (1 + c|x|), dV += P dO, dK += dS' q (scaled by scale n b at the
+// end), dn += ln2 dT sL, db += n scale dS' x.
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
-  constexpr int C4 = D / 4, H4 = C4 / 2;
+__global__ __launch_bounds__(bwd_threads<D>()) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
+  constexpr int P = bwd_parts<D>(), C4 = D / 4, CP = C4 / P, NT = bwd_threads<D>(), NWV = NT / 64;
   __shared__ f32x4 qs[kF32Tile * C4], dos[kF32Tile * C4];
   __shared__ float ms[kF32Tile], dls[kF32Tile];
-  __shared__ float red[2][4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = tid & 1;
+  __shared__ float red[2][NWV];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, part = tid % P;
   const int nkb = dkdv_key_blocks(p.N);
   const int kb = blockIdx.x % nkb, bhk = blockIdx.x / nkb;
   const int b = bhk % p.B, hk = bhk / p.B;
   const int G = p.Hq / p.Hkv;
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
   const int N = sv.N;
-  const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
+  const int64_t PP = static_cast<int64_t>(p.B) * p.Hkv * nkb;
   if (kb * kF32Pair >= N) {  // packed: past the end of a shorter document
     if (tid == 0) {
       p.partials[static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
-      p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
+      p.partials[PP + static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
     }
     return;
   }
-  const int key = kb * kF32Pair + (tid >> 1);
+  const int key = kb * kF32Pair + tid / P;
   const float* kg = static_cast<const float*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
   const float* vg = static_cast<const float*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
-  f32x4 kh[H4], vh[H4], dkh[H4], dvh[H4];
+  f32x4 kh[CP], vh[CP], dkh[CP], dvh[CP];
 #pragma unroll
-  for (int c4 = 0; c4 < H4; ++c4) {
-    const int col = 4 * (half * H4 + c4);
+  for (int c4 = 0; c4 < CP; ++c4) {
+    const int col = 4 * (part * CP + c4);
     kh[c4] = key < N ? ld4(kg + key * p.k.ss + col) : f32x4{0.f, 0.f, 0.f, 0.f};
     vh[c4] = key < N ? ld4(vg + key * p.v.ss + col) : f32x4{0.f, 0.f, 0.f, 0.f};
     dkh[c4] = dvh[c4] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const float n = *p.n_ptr, c = p.scale * *p.b_ptr;
-  float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;  // Kahan sums (lanes with half == 0)
+  float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;  // Kahan sums (lanes with part == 0)
   const int qstart = CAUSAL ? kb * kF32Pair : 0;
   for (int g = 0; g < G; ++g) {
     const int h = hk * G + g;
@@ -192,7 +215,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
     const int64_t mr = sv.mrow(b, h, p.Hq, p.T, p.N);
     for (int q0 = qstart; q0 < N; q0 += kF32Tile) {
       __syncthreads();  // the previous tile is consumed
-      for (int idx = tid; idx < kF32Tile * C4; idx += 256) {
+      for (int idx = tid; idx < kF32Tile * C4; idx += NT) {
         const int row = min(q0 + idx / C4, N - 1), c4 = idx % C4;
         qs[idx] = ld4(qg + row * p.q.ss + 4 * c4);
         dos[idx] = ld4(dog + row * p.dout.ss + 4 * c4);
@@ -206,10 +229,10 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
       const int qn = min(kF32Tile, N - q0);
       for (int r = 0; r < qn; ++r) {
         const int qi = q0 + r;
-        const f32x4* qrow = qs + r * C4 + half * H4;
-        const f32x4* drow = dos + r * C4 + half * H4;
-        const float sh = half_dot<H4>(kh, qrow), dph = half_dot<H4>(vh, drow);
-        const float s = sh + __shfl_xor(sh, 1, 64), dp = dph + __shfl_xor(dph, 1, 64);
+        const f32x4* qrow = qs + r * C4 + part * CP;
+        const f32x4* drow = dos + r * C4 + part * CP;
+        const float s = sum_parts<P>(part_dot<CP>(kh, qrow));
+        const float dp = sum_parts<P>(part_dot<CP>(vh, drow));
         if (key < N && (!CAUSAL || key <= qi)) {
           const float u1 = fmaf(c, fabsf(s), 1.f);
           const float sl = ssa_sl(s, u1);
@@ -217,11 +240,11 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
           const float dt = pv * (dp - dls[r]);
           const float dsp = dt * fast_rcp(u1);
 #pragma unroll
-          for (int c4 = 0; c4 < H4; ++c4) {
+          for (int c4 = 0; c4 < CP; ++c4) {
             dvh[c4] += pv * drow[c4];
             dkh[c4] += dsp * qrow[c4];
           }
-          if (half == 0) {
+          if (part == 0) {
             const float y = dt * sl - dn_c, t = dn_acc + y;
             dn_c = (t - dn_acc) - y;
             dn_acc = t;
@@ -238,13 +261,13 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
     float* dkr = static_cast<float*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh + key * p.dk.ss;
     float* dvr = static_cast<float*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh + key * p.dv.ss;
 #pragma unroll
-    for (int c4 = 0; c4 < H4; ++c4) {
-      const int col = 4 * (half * H4 + c4);
+    for (int c4 = 0; c4 < CP; ++c4) {
+      const int col = 4 * (part * CP + c4);
       st4(dkr + col, dkh[c4] * ks_);
       st4(dvr + col, dvh[c4]);
     }
   }
-  // dn / db partial of this key block: lane butterfly, then waves in order
+  // dn / db partial of this key block: lane butterfly, then the waves in order
   float pdn = dn_acc - dn_c, pdb = db_acc - db_c;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -257,22 +280,26 @@ __global__ __launch_bounds__(256) void ssa_bwd_dkdv_f32_kernel(BwdParams p) {
   }
   __syncthreads();
   if (tid == 0) {
-    const float sdn = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-    const float sdb = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    float sdn = 0.f, sdb = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) {
+      sdn += red[0][w];
+      sdb += red[1][w];
+    }
     p.partials[static_cast<int64_t>(bhk) * nkb + kb] = kLn2 * sdn;
-    p.partials[P + static_cast<int64_t>(bhk) * nkb + kb] = n * p.scale * sdb;
+    p.partials[PP + static_cast<int64_t>(bhk) * nkb + kb] = n * p.scale * sdb;
   }
 }
 
 // ---------------------------------------------------------------------------
-// dQ for 128 query rows of one (batch, q-head): two lanes per row, each
-// holding half of q, dO and dQ; K / V tiles of 32 keys in LDS; the scores and
-// dP are recomputed (dQ += scale n b dS' k).
+// dQ for 128 query rows of one (batch, q-head): P lanes per row, each holding
+// its share of q, dO and dQ; K / V tiles of 32 keys in LDS; the scores and dP
+// are recomputed (dQ += scale n b dS' k).
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void ssa_bwd_dq_f32_kernel(BwdParams p) {
-  constexpr int C4 = D / 4, H4 = C4 / 2;
+__global__ __launch_bounds__(bwd_threads<D>()) void ssa_bwd_dq_f32_kernel(BwdParams p) {
+  constexpr int P = bwd_parts<D>(), C4 = D / 4, CP = C4 / P, NT = bwd_threads<D>();
   __shared__ f32x4 ks[kF32Tile * C4], vs[kF32Tile * C4];
-  const int tid = threadIdx.x, half = tid & 1;
+  const int tid = threadIdx.x, part = tid % P;
   const int nqb = (p.N + kF32Pair - 1) / kF32Pair;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh % p.B, h = bh / p.B, hk = h / (p.Hq / p.Hkv);
@@ -280,15 +307,15 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_f32_kernel(BwdParams p) {
   const int N = sv.N;
   const int q0 = qb * kF32Pair;
   if (q0 >= N) return;
-  const int i = q0 + (tid >> 1);
+  const int i = q0 + tid / P;
   const float* qg = static_cast<const float*>(p.q.ptr) + sv.off(p.q, b) + h * p.q.sh;
   const float* dog = static_cast<const float*>(p.dout.ptr) + sv.off(p.dout, b) + h * p.dout.sh;
   const float* kg = static_cast<const float*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
   const float* vg = static_cast<const float*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
-  f32x4 qh[H4], doh[H4], dqh[H4];
+  f32x4 qh[CP], doh[CP], dqh[CP];
 #pragma unroll
-  for (int c4 = 0; c4 < H4; ++c4) {
-    const int col = 4 * (half * H4 + c4);
+  for (int c4 = 0; c4 < CP; ++c4) {
+    const int col = 4 * (part * CP + c4);
     qh[c4] = i < N ? ld4(qg + i * p.q.ss + col) : f32x4{0.f, 0.f, 0.f, 0.f};
     doh[c4] = i < N ? ld4(dog + i * p.dout.ss + col) : f32x4{0.f, 0.f, 0.f, 0.f};
     dqh[c4] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -299,7 +326,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_f32_kernel(BwdParams p) {
   const int kv_end = CAUSAL ? min(N, q0 + kF32Pair) : N;
   for (int k0 = 0; k0 < kv_end; k0 += kF32Tile) {
     __syncthreads();
-    for (int idx = tid; idx < kF32Tile * C4; idx += 256) {
+    for (int idx = tid; idx < kF32Tile * C4; idx += NT) {
       const int row = min(k0 + idx / C4, N - 1), c4 = idx % C4;
       ks[idx] = ld4(kg + row * p.k.ss + 4 * c4);
       vs[idx] = ld4(vg + row * p.v.ss + 4 * c4);
@@ -307,15 +334,15 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_f32_kernel(BwdParams p) {
     __syncthreads();
     const int kn = min(kF32Tile, kv_end - k0);
     for (int j = 0; j < kn; ++j) {
-      const f32x4* krow = ks + j * C4 + half * H4;
-      const float sh = half_dot<H4>(qh, krow), dph = half_dot<H4>(doh, vs + j * C4 + half * H4);
-      const float s = sh + __shfl_xor(sh, 1, 64), dp = dph + __shfl_xor(dph, 1, 64);
+      const f32x4* krow = ks + j * C4 + part * CP;
+      const float s = sum_parts<P>(part_dot<CP>(qh, krow));
+      const float dp = sum_parts<P>(part_dot<CP>(doh, vs + j * C4 + part * CP));
       if (i < N && (!CAUSAL || k0 + j <= i)) {
         const float u1 = fmaf(c, fabsf(s), 1.f);
         const float pv = fast_exp2(fmaf(n, ssa_sl(s, u1), -mi));
         const float dsp = pv * (dp - di) * fast_rcp(u1);
 #pragma unroll
-        for (int c4 = 0; c4 < H4; ++c4) dqh[c4] += dsp * krow[c4];
+        for (int c4 = 0; c4 < CP; ++c4) dqh[c4] += dsp * krow[c4];
       }
     }
   }
@@ -323,36 +350,37 @@ __global__ __launch_bounds__(256) void ssa_bwd_dq_f32_kernel(BwdParams p) {
     const float qs_ = p.scale * n * *p.b_ptr;
     float* dqr = static_cast<float*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + i * p.dq.ss;
 #pragma unroll
-    for (int c4 = 0; c4 < H4; ++c4) st4(dqr + 4 * (half * H4 + c4), dqh[c4] * qs_);
+    for (int c4 = 0; c4 < CP; ++c4) st4(dqr + 4 * (part * CP + c4), dqh[c4] * qs_);
   }
 }
 
-#define SSA_F32_DISPATCH(KERNEL, GRID, BLOCK, P, D, CAUSAL, S)                                     \
-  switch (D) {                                                                                     \
-    case 16:                                                                                       \
-      if (CAUSAL) hipLaunchKernelGGL((KERNEL<16, true>), dim3(GRID), dim3(BLOCK), 0, S, P);        \
-      else hipLaunchKernelGGL((KERNEL<16, false>), dim3(GRID), dim3(BLOCK), 0, S, P);              \
-      break;                                                                                       \
-    case 32:                                                                                       \
-      if (CAUSAL) hipLaunchKernelGGL((KERNEL<32, true>), dim3(GRID), dim3(BLOCK), 0, S, P);        \
-      else hipLaunchKernelGGL((KERNEL<32, false>), dim3(GRID), dim3(BLOCK), 0, S, P);              \
-      break;                                                                                       \
-    case 64:                                                                                       \
-      if (CAUSAL) hipLaunchKernelGGL((KERNEL<64, true>), dim3(GRID), dim3(BLOCK), 0, S, P);        \
-      else hipLaunchKernelGGL((KERNEL<64, false>), dim3(GRID), dim3(BLOCK), 0, S, P);              \
-      break;                                                                                       \
-    case 128:                                                                                      \
-      if (CAUSAL) hipLaunchKernelGGL((KERNEL<128, true>), dim3(GRID), dim3(BLOCK), 0, S, P);       \
-      else hipLaunchKernelGGL((KERNEL<128, false>), dim3(GRID), dim3(BLOCK), 0, S, P);             \
-      break;                                                                                       \
-    default: return hipErrorInvalidValue;                                                          \
+// One launch of KERNEL<D, CAUSAL> per supported head dim, THREADS<D>() threads.
+#define SSA_F32_DISPATCH(KERNEL, THREADS, GRID, P, D, CAUSAL, S)                                           \
+  switch (D) {                                                                                             \
+    case 16:                                                                                               \
+      if (CAUSAL) hipLaunchKernelGGL((KERNEL<16, true>), dim3(GRID), dim3(THREADS<16>()), 0, S, P);        \
+      else hipLaunchKernelGGL((KERNEL<16, false>), dim3(GRID), dim3(THREADS<16>()), 0, S, P);              \
+      break;                                                                                               \
+    case 32:                                                                                               \
+      if (CAUSAL) hipLaunchKernelGGL((KERNEL<32, true>), dim3(GRID), dim3(THREADS<32>()), 0, S, P);        \
+      else hipLaunchKernelGGL((KERNEL<32, false>), dim3(GRID), dim3(THREADS<32>()), 0, S, P);              \
+      break;                                                                                               \
+    case 64:                                                                                               \
+      if (CAUSAL) hipLaunchKernelGGL((KERNEL<64, true>), dim3(GRID), dim3(THREADS<64>()), 0, S, P);        \
+      else hipLaunchKernelGGL((KERNEL<64, false>), dim3(GRID), dim3(THREADS<64>()), 0, S, P);              \
+      break;                                                                                               \
+    case 128:                                                                                              \
+      if (CAUSAL) hipLaunchKernelGGL((KERNEL<128, true>), dim3(GRID), dim3(THREADS<128>()), 0, S, P);      \
+      else hipLaunchKernelGGL((KERNEL<128, false>), dim3(GRID), dim3(THREADS<128>()), 0, S, P);            \
+      break;                                                                                               \
+    default: return hipErrorInvalidValue;                                                                  \
   }
 
 }  // namespace
 
 hipError_t launch_fwd_f32(const FwdParams& p, int D, bool causal, hipStream_t s) {
   const int grid = (p.N + kF32Rows - 1) / kF32Rows * p.B * p.Hq;
-  SSA_F32_DISPATCH(ssa_fwd_f32_kernel, grid, kF32Rows, p, D, causal, s)
+  SSA_F32_DISPATCH(ssa_fwd_f32_kernel, fwd_threads, grid, p, D, causal, s)
   return hipGetLastError();
 }
 
@@ -372,13 +400,13 @@ hipError_t launch_bwd_preprocess_f32(const BwdParams& p, int D, hipStream_t s) {
 
 hipError_t launch_bwd_dkdv_f32(const BwdParams& p, int D, bool causal, hipStream_t s) {
   const int grid = dkdv_key_blocks(p.N) * p.B * p.Hkv;
-  SSA_F32_DISPATCH(ssa_bwd_dkdv_f32_kernel, grid, 256, p, D, causal, s)
+  SSA_F32_DISPATCH(ssa_bwd_dkdv_f32_kernel, bwd_threads, grid, p, D, causal, s)
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_dq_f32(const BwdParams& p, int D, bool causal, hipStream_t s) {
   const int grid = (p.N + kF32Pair - 1) / kF32Pair * p.B * p.Hq;
-  SSA_F32_DISPATCH(ssa_bwd_dq_f32_kernel, grid, 256, p, D, causal, s)
+  SSA_F32_DISPATCH(ssa_bwd_dq_f32_kernel, bwd_threads, grid, p, D, causal, s)
   return hipGetLastError();
 }
 
