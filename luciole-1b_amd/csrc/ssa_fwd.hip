@@ -259,8 +259,12 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
   // elements of key block 0 of S_i are transformed; chunks g >= NP build
   // S_{i+1} (two independent chains) alongside key block 1, so P_{i-1} and the
   // first half of S_i are dead before S_{i+1} is allocated.  The rare slow
-  // path (running max moves) recomputes S_i from K_i, still in LDS.
-  auto iteration_fast = [&](int i) {
+  // path (running max moves) recomputes S_i from K_i, still in LDS.  MASKED:
+  // the same iteration on a tile that needs masks (the causal diagonal band,
+  // the sequence end): p is zeroed outside the mask, in the pipeline and in
+  // the slow path, and every MFMA runs (a masked block adds zeros).
+  auto iteration_fast = [&](int i, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     typedef T v4 __attribute__((ext_vector_type(4)));
     constexpr int NP = 4 * ND32, NS = 2 * ND16, NG = NP + NS, EPC = 32 / NG;
     wait_vm<0>();  // tile i + 1
@@ -297,11 +301,22 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
         pin(Lv[E]);
       }
     };
+    // Element (kb, r) of S_i holds key i BN + 32 kb + crow(r, hh), crow(r, hh) =
+    // crow(r, 0) + 4 hh; it is valid (key < N and, causal, key <= qrow) when
+    // crow(r, 0) <= lim[kb], a per-lane bound: one compare with a constant.
+    int lim[2] = {0, 0};
+    if constexpr (MASKED) {
+      const int last = CAUSAL ? min(qrow, N - 1) : N - 1;
+      lim[0] = last - i * BN - 4 * hh;
+      lim[1] = lim[0] - 32;
+    }
+    auto valid_key = [&](int kb, int r) { return crow(r, 0) <= lim[kb]; };
     auto stage_b = [&](auto ec) {
       constexpr int E = decltype(ec)::value;
       if constexpr (E < 32) {
         const float x = sc[E / 16][E % 16];
         pvv[E] = fast_exp2(fmaf(n, copysignf(Lv[E], x), neg_m));
+        if constexpr (MASKED) pvv[E] = valid_key(E / 16, E % 16) ? pvv[E] : 0.f;
         pin(pvv[E]);
       }
     };
@@ -358,7 +373,10 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
 #pragma unroll
         for (int ds = 0; ds < ND16; ++ds) so = mfma32(tile_read_row<D, v8>(ki, kb, ds), qf[ds], so);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) z = fmaxf(z, NPOS ? so[r] : -so[r]);
+        for (int r = 0; r < 16; ++r) {
+          const float zr = NPOS ? so[r] : -so[r];
+          z = fmaxf(z, !MASKED || valid_key(kb, r) ? zr : -INFINITY);
+        }
       }
       z = pair_max(z);
       const float sst = NPOS ? z : -z;
@@ -379,7 +397,8 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
         for (int r = 0; r < 16; ++r) {
           const float x = so[r];
           const float sl = copysignf(fast_log2(fmaf(c, fabsf(x), 1.f)), x);
-          const float pv = fast_exp2(fmaf(n, sl, -m_run));
+          float pv = fast_exp2(fmaf(n, sl, -m_run));
+          if constexpr (MASKED) pv = valid_key(kb, r) ? pv : 0.f;
           psum += pv;
           pc[kb][r >> 3][r & 7] = static_cast<T>(pv);
         }
@@ -398,7 +417,11 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
   // Iterations with tile i + 1 < nfull keep every stream unmasked.
   iteration(0, std::true_type{}, std::true_type{});
   int i = 1;
-  for (; i + 1 < nfull; ++i) iteration_fast(i);
+  // Iterations whose tile i needs masks run the masked fast iteration while
+  // tile i + 1 exists and this wave has valid keys in tile i; the last two
+  // (and a wave's tiles past its rows) run the generic one.
+  for (; i + 1 < nfull; ++i) iteration_fast(i, std::false_type{});
+  for (; i + 1 < NT && i < Tw; ++i) iteration_fast(i, std::true_type{});
   for (; i <= NT; ++i) iteration(i, std::true_type{}, std::false_type{});
 
   const float l_tot = pair_sum(l_run);
