@@ -37,6 +37,13 @@ HIPCC_FLAGS = [
     "-ffp-contract=fast",
 ]
 
+# Per-source additions.  ssa_bwd.hip: builtin MFMAs write arch VGPRs (the
+# VALU reads S and dP there without copies); the dK/dV accumulators are held in
+# AGPRs by the inline assembly of ssa_common.hpp (mfma32_acc / acc_fence).
+SOURCE_FLAGS = {
+    "ssa_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -46,7 +53,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path, extra: list[str]) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
@@ -58,7 +65,8 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> None:
 
 def _device_asm(src: Path, out: Path, extra: list[str]) -> None:
     """The gfx950 assembly of one source (for the wait-state check)."""
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "--cuda-device-only", "-S", str(src),
+           "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
@@ -85,7 +93,7 @@ def build_library(extra_flags: list[str] | None = None, jobs: int | None = None)
     sites = _hazards.check_files(asms)
     if sites:
         lines = "\n".join(f"  {f}: {fn}: {ws} wait state(s), {need} needed: {ins}" for f, fn, ws, need, ins in sites[:20])
-        raise RuntimeError(f"{len(sites)} vector-memory instruction(s) read a register too soon after its write "
+        raise RuntimeError(f"{len(sites)} instruction(s) read a register too soon after its write "
                            f"(SSA/_hazards.py):\n{lines}")
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]

@@ -17,6 +17,14 @@ With fewer, the memory instruction can read the register's previous value
 and so access a wrong address.  ``scan_asm`` walks a device .s file in
 program order (a label does not reset the window, so fall-through paths are
 covered) and returns every site with fewer wait states than required.
+
+The dK/dV accumulators are MFMAs issued from inline assembly into AGPRs
+(mfma32_acc / acc_fence in csrc/ssa_common.hpp), which the compiler's hazard
+recognizer does not see either.  ``scan_agpr`` checks them on the control-flow
+graph of each function: every such MFMA accumulates in place (dst = srcC, both
+AGPR; srcA / srcB VGPR) right after its own s_nop of at least 2 wait states,
+and every other instruction that names one of their AGPRs is reached, on every
+path, at least ACC_READ_WAIT wait states after the last of them.
 """
 
 from __future__ import annotations
@@ -28,6 +36,8 @@ VMEM = re.compile(r"^(buffer_|global_|flat_|scratch_)")
 LDS_DMA = re.compile(r"^(buffer_\w+.*\blds\b|global_load_lds_)")
 VALU_SGPR_WAIT = 5
 M0_LDS_DMA_WAIT = 1
+ACC_MFMA_SRC_WAIT = 2   # VALU write of an MFMA source -> MFMA
+ACC_READ_WAIT = 19      # XDL write (up to 16 passes) -> any other access of its result
 
 
 def _sregs(tok: str) -> set:
@@ -105,9 +115,129 @@ def scan_asm(text: str) -> list:
     return sites
 
 
+_ACC_FORM = re.compile(r"^v_mfma_\w+ (a\[\d+:\d+\]), v\[\d+:\d+\], v\[\d+:\d+\], (a\[\d+:\d+\])$")
+_AREG = re.compile(r"\ba(\d+)\b|\ba\[(\d+):(\d+)\]")
+_BRANCH = re.compile(r"^s_(c?branch)\w* (\.L\w+)")
+_INF = 1 << 30
+
+
+def _aregs(ins: str) -> set:
+    out = set()
+    for one, lo, hi in _AREG.findall(ins):
+        out |= {int(one)} if one else set(range(int(lo), int(hi) + 1))
+    return out
+
+
+def _functions(text: str):
+    """(name, [(instruction, from_inline_asm) or label]) of each function."""
+    name, body, in_asm = None, [], False
+    for raw in text.split("\n"):
+        m = re.match(r"^(_Z\S+|[A-Za-z_]\w*):", raw)
+        if m and not raw.startswith((".", "\t")):
+            if name:
+                yield name, body
+            name, body, in_asm = m.group(1), [], False
+            continue
+        if name is None:
+            continue
+        if raw.strip().startswith(".Lfunc_end"):
+            yield name, body
+            name = None
+            continue
+        if ";;#ASMSTART" in raw:
+            in_asm = True
+        elif ";;#ASMEND" in raw:
+            in_asm = False
+        lab = re.match(r"^(\.L\w+):", raw)
+        if lab:
+            body.append(lab.group(1))
+            continue
+        s = raw.split(";")[0].strip()
+        if s and not s.startswith("."):
+            body.append((s, in_asm))
+    if name:
+        yield name, body
+
+
+def scan_agpr(text: str) -> list:
+    """Sites of one device assembly file where an inline-assembly AGPR
+    accumulation is not covered: (function, wait states, needed, instruction)."""
+    sites = []
+    for func, body in _functions(text):
+        # basic blocks: split at labels and after branches / ends
+        blocks, labels, cur = [], {}, []
+        for item in body:
+            if isinstance(item, str):
+                if cur:
+                    blocks.append(cur)
+                    cur = []
+                labels[item] = len(blocks)
+                continue
+            cur.append(item)
+            if item[0].startswith(("s_branch", "s_cbranch", "s_endpgm", "s_setpc")):
+                blocks.append(cur)
+                cur = []
+        if cur:
+            blocks.append(cur)
+        acc, acc_regs = set(), set()
+        for bi, blk in enumerate(blocks):
+            for k, (ins, in_asm) in enumerate(blk):
+                if in_asm and ins.startswith("v_mfma") and _aregs(ins):
+                    acc.add((bi, k))
+                    m = _ACC_FORM.match(ins)
+                    if not m or m.group(1) != m.group(2):
+                        sites.append((func, 0, ACC_MFMA_SRC_WAIT, ins))
+                        continue
+                    acc_regs |= _aregs(m.group(1))
+                    prev = blk[k - 1][0] if k else ""
+                    pm = re.match(r"s_nop (\d+)", prev)
+                    if not pm or int(pm.group(1), 0) + 1 < ACC_MFMA_SRC_WAIT:
+                        sites.append((func, int(pm.group(1), 0) + 1 if pm else 0, ACC_MFMA_SRC_WAIT, ins))
+        if not acc:
+            continue
+        succ = []
+        for bi, blk in enumerate(blocks):
+            last = blk[-1][0]
+            nxt = []
+            m = _BRANCH.match(last)
+            if m and m.group(2) in labels:
+                nxt.append(labels[m.group(2)])
+            if not last.startswith(("s_branch", "s_endpgm", "s_setpc")) and bi + 1 < len(blocks):
+                nxt.append(bi + 1)
+            succ.append(nxt)
+
+        def walk(bi, dist, report):
+            for k, (ins, _) in enumerate(blocks[bi]):
+                if (bi, k) in acc:
+                    dist = 0
+                    continue
+                if report and dist < ACC_READ_WAIT and _aregs(ins) & acc_regs:
+                    sites.append((func, dist, ACC_READ_WAIT, ins))
+                nop = re.match(r"s_nop (\d+)", ins)
+                dist = min(_INF, dist + (int(nop.group(1), 0) + 1 if nop else 1))
+            return dist
+
+        # fewest wait states since the last accumulation, over all paths into each block
+        entry = [None] * len(blocks)
+        entry[0] = _INF
+        work = [0]
+        while work:
+            bi = work.pop()
+            out = walk(bi, entry[bi], False)
+            for nb in succ[bi]:
+                if entry[nb] is None or out < entry[nb]:
+                    entry[nb] = out
+                    work.append(nb)
+        for bi in range(len(blocks)):
+            if entry[bi] is not None:
+                walk(bi, entry[bi], True)
+    return sites
+
+
 def check_files(paths) -> list:
     out = []
     for p in paths:
-        for site in scan_asm(Path(p).read_text()):
+        text = Path(p).read_text()
+        for site in scan_asm(text) + scan_agpr(text):
             out.append((Path(p).name, *site))
     return out

@@ -284,7 +284,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
                      : zero8<v8>();
   }
 
-  f32x16 dk[ND32], dv[ND32];
+  f32x16 dk[ND32], dv[ND32];  // accumulation registers: mfma32_acc / acc_fence only
 #pragma unroll
   for (int i = 0; i < ND32; ++i) {
     dk[i] = f32x16{};
@@ -294,8 +294,17 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // S, dP of sub-tiles j and j + 1.  Zero-initialised: a skipped step leaves
   // them as they were, and the masked fast slot multiplies their entries by a
   // zero P, which must stay zero (finite operands).
-  f32x16 sc = f32x16{}, dc = f32x16{}, sn = f32x16{}, dn2 = f32x16{};
-  v8 pa[2], sa[2], pa2[2], sa2[2];  // P^T, dS'^T operands of sub-tiles j - 1 and j
+  // Two sets of each, used alternately by consecutive fast slots so that the
+  // steady state moves nothing between registers; the generic slot and the
+  // ends of the fast runs use set 0 as current (sc, dc, pa, sa) and set 1 as
+  // next (sn, dn2, pa2, sa2), and rotate() copies next into current.
+  f32x16 s_set[2] = {f32x16{}, f32x16{}}, d_set[2] = {f32x16{}, f32x16{}};
+  v8 p_set[2][2], a_set[2][2];  // P^T, dS'^T operands of sub-tiles j - 1 and j
+  f32x16 &sc = s_set[0], &sn = s_set[1], &dc = d_set[0], &dn2 = d_set[1];
+  v8(&pa)[2] = p_set[0];
+  v8(&pa2)[2] = p_set[1];
+  v8(&sa)[2] = a_set[0];
+  v8(&sa2)[2] = a_set[1];
 
   auto kahan = [&](float tdn, float tdb) {
     const float y = tdn - dn_c, t = dn_acc + y;
@@ -339,8 +348,8 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         const v4 dhi = tile_read_tr<D, v4>(td, 0, ks, 1, db);
         const v4 qlo = tile_read_tr<D, v4>(tq, 0, ks, 0, db);
         const v4 qhi = tile_read_tr<D, v4>(tq, 0, ks, 1, db);
-        dv[db] = mfma32(pp[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7), dv[db]);
-        dk[db] = mfma32(ss[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7), dk[db]);
+        mfma32_acc(dv[db], pp[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7));
+        mfma32_acc(dk[db], ss[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     }
   };
@@ -404,9 +413,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const i32x4_t ds_rs = raw_rsrc(ds_head0);
   const uint32_t ds_voff = (ds_lane + (16 * hh) * 8) * 2;
   const int ds_tph1k = static_cast<int>(ds_tph * 1024);
-  auto ds_store = [&](const StepWalk& w, auto unmasked_tag) {
+  auto ds_store = [&](const StepWalk& w, const v8 (&s2)[2], auto unmasked_tag) {
     const int q0 = qstart + (decltype(unmasked_tag)::value ? w.sub_unmasked(nlo) : w.sub(nlo, nsub)) * BMQ;
-    const u32x4 s0 = __builtin_bit_cast(u32x4, sa2[0]), s1 = __builtin_bit_cast(u32x4, sa2[1]);
+    const u32x4 s0 = __builtin_bit_cast(u32x4, s2[0]), s1 = __builtin_bit_cast(u32x4, s2[1]);
     if constexpr (OFF32) {
       const int qi = q0 >> 5;
       const int soff = __builtin_amdgcn_readfirstlane(w.g * ds_tph1k +
@@ -431,7 +440,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         elementwise(j, std::true_type{});
       else
         elementwise(j, std::false_type{});
-      if constexpr (DS) ds_store(wc, std::false_type{});
+      if constexpr (DS) ds_store(wc, sa2, std::false_type{});
     } else {
       // the masked fast slot after this one runs dV/dK of step j
       // unconditionally: zero operands add nothing
@@ -447,8 +456,16 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // last sub-tile, a key block at the sequence end): P is zeroed outside the
   // mask, every MFMA runs (a skipped step contributes zeros), and only a step
   // with a valid pair stores its dS' tile.
-  auto slot_fast = [&](int j, auto masked_tag) {
+  // PH: which state set is current (set PH ^ 1 is next); the slot leaves the
+  // next sets filled for slot j + 1, which runs with the phase flipped.
+  auto slot_fast = [&](int j, auto masked_tag, auto phase_tag) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr int PH = decltype(phase_tag)::value;
+    f32x16 &sc = s_set[PH], &sn = s_set[PH ^ 1], &dc = d_set[PH], &dn2 = d_set[PH ^ 1];
+    v8(&pa)[2] = p_set[PH];
+    v8(&pa2)[2] = p_set[PH ^ 1];
+    v8(&sa)[2] = a_set[PH];
+    v8(&sa2)[2] = a_set[PH ^ 1];
     constexpr int NG = 4 * ND32 + 2 * ND16;  // MFMAs per slot
     constexpr int STRIDE = 32 / NG;           // ticks per MFMA
     // Sub-tile j + 1 (issued in slot j - 1).  The vector-memory counter also
@@ -501,9 +518,9 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
       if constexpr (Gi < 4 * ND32) {
         constexpr int idx = Gi / 2, ks = idx / ND32, db = idx % ND32;
         if constexpr (Gi % 2 == 0)
-          dv[db] = mfma32(pa[ks], ops[Gi % 3], dv[db]);
+          mfma32_acc(dv[db], pa[ks], ops[Gi % 3]);
         else
-          dk[db] = mfma32(sa[ks], ops[Gi % 3], dk[db]);
+          mfma32_acc(dk[db], sa[ks], ops[Gi % 3]);
       } else {
         constexpr int h = Gi - 4 * ND32, ds = h / 2;
         if constexpr (h % 2 == 0)
@@ -582,13 +599,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     }(std::make_integer_sequence<int, 32>{});
     kahan(tdn, tdb);
     if constexpr (DS) {
-      if (!MASKED || !skipped(j)) ds_store(wc, std::integral_constant<bool, !MASKED>{});
+      if (!MASKED || !skipped(j)) ds_store(wc, sa2, std::integral_constant<bool, !MASKED>{});
     }
     if constexpr (MASKED)
       wc.next(per_m, per_u, G);
     else
       wc.next_unmasked(per_u);
-    rotate();
   };
 
   // prologue: sub-tiles 0 and 1 in flight, S/dP of sub-tile 0
@@ -602,13 +618,27 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // that step ends the sequence, unmasked fast slots, generic drain
   slot_generic(0);
   int j = 1;
-  for (; j <= nmasked && j + 1 < nsteps; ++j) slot_fast(j, std::true_type{});
+  // fast slots j < jend in pairs (phases 0, 1); an odd last one ends with the
+  // copy that puts its next sets in place as set 0
+  auto fast_run = [&](int jend, auto masked_tag) __attribute__((always_inline)) {
+    for (; j + 1 < jend; j += 2) {
+      slot_fast(j, masked_tag, std::integral_constant<int, 0>{});
+      slot_fast(j + 1, masked_tag, std::integral_constant<int, 1>{});
+    }
+    if (j < jend) {
+      slot_fast(j, masked_tag, std::integral_constant<int, 0>{});
+      rotate();
+      ++j;
+    }
+  };
+  fast_run(min(nmasked + 1, nsteps - 1), std::true_type{});
   for (; j <= nmasked && j <= nsteps; ++j) slot_generic(j);
-  for (; j + 1 < nsteps; ++j) slot_fast(j, std::false_type{});
+  fast_run(nsteps - 1, std::false_type{});
   for (; j <= nsteps; ++j) slot_generic(j);
 
   // Store dK (scaled by scale * n * b; the accumulator holds -dK_raw) and dV.
   __syncthreads();  // every wave is done with the sub-tile ring (no loads in flight)
+  acc_fence(dk, dv);
   {
     const uint32_t tile = lds0 + wave * key_block_tile_bytes<D>();
     T* dkr = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;

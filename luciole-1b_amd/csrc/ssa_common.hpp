@@ -43,6 +43,32 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// c += a b into a block that lives in accumulation registers (AGPRs) from its
+// zero initialisation to acc_fence().  A kernel that keeps long-lived
+// accumulators this way lets the compiler place every builtin MFMA result in
+// arch VGPRs (ssa_bwd.hip is built with -amdgpu-mfma-vgpr-form), where the
+// VALU reads it without a copy.  The compiler does not see inside the asm, so
+// its two hazards are covered here and checked on the built assembly
+// (SSA/_hazards.py): the s_nop gives the 2 wait states a VALU write of a
+// source (or of the zeroed accumulator) needs before the matrix core reads it;
+// acc_fence() puts 24 wait states between the last accumulation and any other
+// access to the block.  Only these two statements may touch the block.
+__device__ __forceinline__ void mfma32_acc(f32x16& c, bf16x8 a, bf16x8 b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma32_acc(f32x16& c, f16x8 a, f16x8 b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+// After the last mfma32_acc on x and y, before their values are read.  The
+// volatile statements keep their order, and each one names its blocks as
+// read-write, so every read of x[i] / y[i] follows the NOPs.
+template <int N>
+__device__ __forceinline__ void acc_fence(f32x16 (&x)[N], f32x16 (&y)[N]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(x[0]), "+a"(y[0]));
+#pragma unroll
+  for (int i = 1; i < N; ++i) asm volatile("" : "+a"(x[i]), "+a"(y[i]));
+}
+
 // Row (within a 32-row accumulator block) held in accumulator entry r by lane half hh.
 __device__ __forceinline__ int crow(int r, int hh) { return ((r >> 2) << 3) + (hh << 2) + (r & 3); }
 

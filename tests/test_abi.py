@@ -450,6 +450,44 @@ def test_hazard_scan_flags_short_waits():
     assert sites(far) == []
 
 
+def test_agpr_scan_follows_every_path():
+    """SSA/_hazards.py's check of the inline-assembly AGPR accumulations:
+    in-place form after its own s_nop, and no other access to the block
+    within 19 wait states of the last accumulation on any path (a loop's
+    back edge and a branch around the fence included)."""
+    from SSA import _hazards
+
+    def acc(dst="a[0:15]", src_c="a[0:15]", nop="s_nop 1"):
+        return [";;#ASMSTART", nop, f"v_mfma_f32_32x32x16_bf16 {dst}, v[2:5], v[6:9], {src_c}", ";;#ASMEND"]
+
+    fence = [";;#ASMSTART", "s_nop 7", "s_nop 7", "s_nop 7", ";;#ASMEND"]
+
+    def sites(body):
+        text = "_Zk:\n" + "\n".join(ln if ln.startswith(".L") else "\t" + ln for ln in body) + "\n.Lfunc_end0:\n"
+        return [(s[1], s[2], s[3].split()[0]) for s in _hazards.scan_agpr(text)]
+
+    loop = ["v_accvgpr_write_b32 a0, 0", ".LBB0_1:", *acc(), "v_add_f32_e32 v3, v3, v3",
+            "s_cbranch_scc1 .LBB0_1"]
+    assert sites(loop + fence + ["v_accvgpr_read_b32 v10, a3", "s_endpgm"]) == []
+    # the read without the fence: 2 wait states after the accumulation
+    assert sites(loop + ["v_accvgpr_read_b32 v10, a3", "s_endpgm"]) == [(2, 19, "v_accvgpr_read_b32")]
+    # a branch that skips the fence reaches the read 3 wait states after it
+    skip = loop + ["s_cbranch_vccnz .LBB0_3"] + fence + [".LBB0_3:", "v_accvgpr_read_b32 v10, a3", "s_endpgm"]
+    assert sites(skip) == [(3, 19, "v_accvgpr_read_b32")]
+    # an access of another block is not constrained; the loop's back edge is
+    # (a copy at the top of the loop, 2 wait states after the previous pass)
+    assert sites(loop + ["v_accvgpr_read_b32 v10, a16", "s_endpgm"]) == []
+    back = ["v_accvgpr_write_b32 a0, 0", ".LBB0_1:", "v_accvgpr_read_b32 v11, a5", *acc(),
+            "v_add_f32_e32 v3, v3, v3", "s_cbranch_scc1 .LBB0_1", *fence, "s_endpgm"]
+    assert sites(back) == [(2, 19, "v_accvgpr_read_b32")]
+    # an accumulation without its NOP, or not in place
+    assert sites([*acc(nop="v_add_f32_e32 v4, v4, v4"), *fence, "s_endpgm"]) == [(0, 2, "v_mfma_f32_32x32x16_bf16")]
+    assert sites([*acc(dst="a[16:31]"), *fence, "s_endpgm"]) == [(0, 2, "v_mfma_f32_32x32x16_bf16")]
+    # a compiler-issued MFMA is the compiler's business
+    assert sites(["v_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[6:9], a[0:15]",
+                  "v_accvgpr_read_b32 v10, a3", "s_endpgm"]) == []
+
+
 def test_built_device_assembly_has_no_short_waits():
     """The assembly the last build() checked (luciole-1b_amd/_build/*.gfx950.s),
     re-scanned: no vector-memory instruction reads a register too soon."""
