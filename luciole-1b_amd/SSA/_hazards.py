@@ -24,7 +24,10 @@ recognizer does not see either.  ``scan_agpr`` checks them on the control-flow
 graph of each function: every such MFMA accumulates in place (dst = srcC, both
 AGPR; srcA / srcB VGPR) right after its own s_nop of at least 2 wait states,
 and every other instruction that names one of their AGPRs is reached, on every
-path, at least ACC_READ_WAIT wait states after the last of them.
+path, at least ACC_READ_WAIT wait states after the last of them; and no
+source VGPR of such an MFMA was written by a compiler-issued MFMA fewer than
+ACC_READ_WAIT wait states before it on any path (the compiler pads that
+hazard only between the MFMAs it sees).
 """
 
 from __future__ import annotations
@@ -119,6 +122,14 @@ _ACC_FORM = re.compile(r"^v_mfma_\w+ (a\[\d+:\d+\]), v\[\d+:\d+\], v\[\d+:\d+\],
 _AREG = re.compile(r"\ba(\d+)\b|\ba\[(\d+):(\d+)\]")
 _BRANCH = re.compile(r"^s_(c?branch)\w* (\.L\w+)")
 _INF = 1 << 30
+
+
+def _vregs(tok: str) -> set:
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", tok) or re.fullmatch(r"v(\d+)()", tok)
+    if not m:
+        return set()
+    lo = int(m.group(1))
+    return set(range(lo, int(m.group(2) or lo) + 1))
 
 
 def _aregs(ins: str) -> set:
@@ -231,6 +242,49 @@ def scan_agpr(text: str) -> list:
         for bi in range(len(blocks)):
             if entry[bi] is not None:
                 walk(bi, entry[bi], True)
+
+        # wait states since a compiler-issued MFMA wrote each VGPR (only those
+        # still under ACC_READ_WAIT), at each block entry: fewest over all paths
+        def mfma_walk(bi, state, report):
+            pos, written = 0, {}
+            for k, (ins, _) in enumerate(blocks[bi]):
+                ops = [t.strip() for t in ins.split(" ", 1)[1].split(",")] if " " in ins else []
+                if (bi, k) in acc:
+                    d = min((pos - written[r] if r in written else state.get(r, _INF) + pos
+                             for r in _vregs(ops[1]) | _vregs(ops[2])), default=_INF)
+                    if report and d < ACC_READ_WAIT:
+                        sites.append((func, d, ACC_READ_WAIT, ins))
+                elif ins.startswith("v_mfma") and ops:
+                    for r in _vregs(ops[0]):
+                        written[r] = pos + 1  # wait states count from the next instruction
+                nop = re.match(r"s_nop (\d+)", ins)
+                pos += int(nop.group(1), 0) + 1 if nop else 1
+            out = {r: d + pos for r, d in state.items() if d + pos < ACC_READ_WAIT}
+            for r, w in written.items():
+                if pos - w < ACC_READ_WAIT:
+                    out[r] = pos - w
+            return out
+
+        ment = [None] * len(blocks)
+        ment[0] = {}
+        work = [0]
+        while work:
+            bi = work.pop()
+            out = mfma_walk(bi, ment[bi], False)
+            for nb in succ[bi]:
+                if ment[nb] is None:
+                    new = dict(out)
+                else:
+                    new = dict(ment[nb])
+                    for r, d in out.items():
+                        if d < new.get(r, _INF):
+                            new[r] = d
+                if new != ment[nb]:
+                    ment[nb] = new
+                    work.append(nb)
+        for bi in range(len(blocks)):
+            if ment[bi] is not None:
+                mfma_walk(bi, ment[bi], True)
     return sites
 
 

@@ -486,6 +486,13 @@ def test_agpr_scan_follows_every_path():
     # a compiler-issued MFMA is the compiler's business
     assert sites(["v_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[6:9], a[0:15]",
                   "v_accvgpr_read_b32 v10, a3", "s_endpgm"]) == []
+    # ... except that its VGPR result may not feed an accumulation too soon,
+    # on any path (here around a loop: written at the bottom, read at the top)
+    mfma_v = "v_mfma_f32_32x32x16_bf16 v[0:15], v[20:23], v[24:27], 0"
+    assert sites([mfma_v, "s_nop 7", *acc(), *fence, "s_endpgm"]) == [(10, 19, "v_mfma_f32_32x32x16_bf16")]
+    assert sites([mfma_v, "s_nop 7", "s_nop 7", "s_nop 3", *acc(), *fence, "s_endpgm"]) == []
+    around = [".LBB0_1:", *acc(), "v_add_f32_e32 v30, v30, v30", mfma_v, "s_cbranch_scc1 .LBB0_1", *fence, "s_endpgm"]
+    assert sites(around) == [(3, 19, "v_mfma_f32_32x32x16_bf16")]
 
 
 def test_built_device_assembly_has_no_short_waits():
