@@ -495,6 +495,49 @@ def test_agpr_scan_follows_every_path():
     assert sites(around) == [(3, 19, "v_mfma_f32_32x32x16_bf16")]
 
 
+_ACC_PROBE = r"""
+#include "ssa_common.hpp"
+using namespace ssa;
+__global__ void acc_probe(float* o, const bf16x8* a) {
+  f32x16 c[1] = {f32x16{}}, d[1] = {f32x16{}};
+  for (int t = 0; t < 4; ++t) {
+    mfma32_acc(c[0], a[threadIdx.x + 128 * t], a[threadIdx.x + 64 + 128 * t]);
+    mfma32_acc(d[0], a[threadIdx.x + 64 + 128 * t], a[threadIdx.x + 128 * t]);
+  }
+#ifdef FENCE
+  acc_fence(c, d);
+#endif
+  for (int i = 0; i < 16; ++i) o[threadIdx.x * 16 + i] = c[0][i] + d[0][i];
+}
+"""
+
+
+def test_agpr_scan_on_compiled_accumulation(tmp_path):
+    """The accumulation helpers of csrc/ssa_common.hpp through the real
+    compiler: without acc_fence() the compiler reads the accumulators right
+    after the last inline-assembly MFMA (it does not know the statement is an
+    MFMA), and the build's scan reports it; with the fence the scan is clean."""
+    import subprocess
+
+    from SSA import _build, _hazards
+
+    try:
+        hipcc = _build._hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    src = tmp_path / "probe.hip"
+    src.write_text(_ACC_PROBE)
+    found = {}
+    for tag, extra in (("plain", []), ("fenced", ["-DFENCE"])):
+        out = tmp_path / f"{tag}.s"
+        cmd = [hipcc, *_build.HIPCC_FLAGS, *_build.SOURCE_FLAGS["ssa_bwd.hip"], f"-I{_build.CSRC}", *extra,
+               "--cuda-device-only", "-S", str(src), "-o", str(out)]
+        subprocess.run(cmd, check=True, capture_output=True, text=True)
+        found[tag] = _hazards.scan_agpr(out.read_text())
+    assert found["fenced"] == []
+    assert found["plain"] and all(ws < need and ins.startswith("v_accvgpr_read") for _, ws, need, ins in found["plain"])
+
+
 def test_built_device_assembly_has_no_short_waits():
     """The assembly the last build() checked (luciole-1b_amd/_build/*.gfx950.s),
     re-scanned: no vector-memory instruction reads a register too soon."""
