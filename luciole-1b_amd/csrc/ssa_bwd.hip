@@ -467,7 +467,6 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     v8(&sa)[2] = a_set[PH];
     v8(&sa2)[2] = a_set[PH ^ 1];
     constexpr int NG = 4 * ND32 + 2 * ND16;  // MFMAs per slot
-    constexpr int STRIDE = 32 / NG;           // ticks per MFMA
     // Sub-tile j + 1 (issued in slot j - 1).  The vector-memory counter also
     // counts stores, in issue order: slot j - 1 ended with its two dS' stores
     // (an unmasked slot always stores; a masked one unless its step was
@@ -533,7 +532,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     //   A: u = 1 + c|x|, L = log2 u, 1/u
     //   B: sL = copysign(L, x), p = exp2(n sL - M)
     //   C1: -dT = p (Delta - dP), -dS' = -dT / u      C2: dn, db sums, bf16 operands
-    // tick 2e: A(e + 2), C1(e); tick 2e + 1: B(e + 1), C2(e)
+    // (the ticks below run the four stages on different elements)
     float Lv[16], rv[16], slv[16], pv[16], dtv[16], dsv[16];
     float tdn = 0.f, tdb = 0.f;
     auto A = [&](int e) {
@@ -573,30 +572,43 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
         sa2[e >> 3][e & 7] = static_cast<T>(dsv[e]);
       }
     };
+    // TK ticks per slot; tick t issues the MFMAs G in [t NG / TK, (t + 1) NG /
+    // TK), each after the operand read two MFMAs ahead, beside four
+    // independent stages on EPT elements each: A(t + 2), B(t + 1), C1(t),
+    // C2(t - 1) in units of EPT elements.  Sixteen ticks at D = 128 (two
+    // MFMAs per tick), eight below (a tick carries more element work where
+    // the MFMAs are fewer).
+    constexpr int TK = D >= 128 ? 16 : 8, EPT = 16 / TK;
     auto tick = [&](auto tc) {
       constexpr int t = decltype(tc)::value;
-      if constexpr (t % STRIDE == 0) {
-        read(std::integral_constant<int, t / STRIDE + 2>{});
-        mfma(std::integral_constant<int, t / STRIDE>{});
-      }
-      constexpr int e = t / 2;
-      if constexpr (t % 2 == 0) {
-        if constexpr (e + 2 < 16) A(e + 2);
-        C1(e);
-      } else {
-        if constexpr (e + 1 < 16) B(e + 1);
-        C2(e);
-      }
+      constexpr int G0 = t * NG / TK, G1 = (t + 1) * NG / TK;
+      [&]<int... g>(std::integer_sequence<int, g...>) {
+        ((read(std::integral_constant<int, G0 + g + 2>{}), mfma(std::integral_constant<int, G0 + g>{})), ...);
+      }(std::make_integer_sequence<int, G1 - G0>{});
+#pragma unroll
+      for (int k = 0; k < EPT; ++k)
+        if (EPT * (t + 2) + k < 16) A(EPT * (t + 2) + k);
+#pragma unroll
+      for (int k = 0; k < EPT; ++k)
+        if (EPT * (t + 1) + k < 16) B(EPT * (t + 1) + k);
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) C1(EPT * t + k);
+#pragma unroll
+      for (int k = 0; k < EPT; ++k)
+        if (t >= 1) C2(EPT * (t - 1) + k);
       __builtin_amdgcn_sched_barrier(0);
     };
     read(std::integral_constant<int, 0>{});
     read(std::integral_constant<int, 1>{});
-    A(0);
-    A(1);
-    B(0);
+#pragma unroll
+    for (int e = 0; e < 2 * EPT; ++e) A(e);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) B(e);
     [&]<int... t>(std::integer_sequence<int, t...>) {
       (tick(std::integral_constant<int, t>{}), ...);
-    }(std::make_integer_sequence<int, 32>{});
+    }(std::make_integer_sequence<int, TK>{});
+#pragma unroll
+    for (int e = 16 - EPT; e < 16; ++e) C2(e);
     kahan(tdn, tdb);
     if constexpr (DS) {
       if (!MASKED || !skipped(j)) ds_store(wc, sa2, std::integral_constant<bool, !MASKED>{});
