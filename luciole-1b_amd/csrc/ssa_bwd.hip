@@ -189,8 +189,10 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     }
     return;
   }
-  const float n = *p.n_ptr;
-  const float c = p.scale * *p.b_ptr;
+  // n and b read once here: a read after the main loop would queue behind its
+  // memory traffic and hold the workgroup's end for the round trip
+  const float n = *p.n_ptr, bv = *p.b_ptr;
+  const float c = p.scale * bv;
   const uint32_t lds0 = lds_addr(smem);
   const RowBase<D> rb(l32, hh);
   const TrBase<D> tb(lane);
@@ -655,7 +657,7 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const uint32_t tile = lds0 + wave * key_block_tile_bytes<D>();
     T* dkr = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;
     T* dvr = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh;
-    store_key_block<T, D>(dk, -(p.scale * n * *p.b_ptr), dkr, p.dk.ss, k0w, N, tile, lane);
+    store_key_block<T, D>(dk, -(p.scale * n * bv), dkr, p.dk.ss, k0w, N, tile, lane);
     store_key_block<T, D>(dv, 1.f, dvr, p.dv.ss, k0w, N, tile, lane);
   }
 
@@ -718,8 +720,10 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
   const char* vg = static_cast<const char*>(p.v.ptr) + (sv.off(p.v, b) + hk * p.v.sh) * 2;
 
-  const float n = *p.n_ptr;
-  const float c = p.scale * *p.b_ptr;
+  // n and b read once here: a read after the main loop would queue behind its
+  // memory traffic and hold the workgroup's end for the round trip
+  const float n = *p.n_ptr, bv = *p.b_ptr;
+  const float c = p.scale * bv;
   const int q0 = qb * BM;
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
@@ -806,7 +810,7 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   for (int t = 0; t < nfull; ++t) tile(t, std::false_type{});
   for (int t = nfull; t < ntiles; ++t) tile(t, std::true_type{});
 
-  const float qscale = p.scale * n * *p.b_ptr;
+  const float qscale = p.scale * n * bv;
   if (qrow < N) {
     T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + qrow * p.dq.ss;
 #pragma unroll
@@ -903,7 +907,6 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l32 = lane & 31, hh = lane >> 5;
   const int nqb = (p.N + BM - 1) / BM;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   int hb, rank;
@@ -913,6 +916,11 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const SeqView sv(p.cu_seqlens, p.T, p.N, b);
   const int N = sv.N;
   if (qb * BM >= N) return;  // packed: past the end of a shorter document
+  // the workspace holds -dS' (the dK/dV kernel's sign convention); n and b
+  // are read before the stream starts (read after it, the two loads queue
+  // behind the workspace traffic and hold the workgroup's end: 25 % of the
+  // pass in the loads-only ablation)
+  const float qscale = -(p.scale * *p.n_ptr * *p.b_ptr);
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t lds_ds = lds0 + NK * KTILE;
   // K tiles: row-swizzled for D = 128 (whole-row loads), block-chunk-major otherwise
@@ -924,7 +932,6 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
 
   const int q0 = qb * BM;
   const int wq0 = q0 + wave * 32;
-  const int qrow = wq0 + l32;
   const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
   const int ntiles = (kv_end + BN - 1) / BN;
   // dS' tiles of this wave's query rows: kj < nkj (loads clamped to kj_max)
@@ -1012,21 +1019,14 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   }
   wait_vm<0>();  // no direct-to-LDS load may outlive the workgroup
 
-  // the workspace holds -dS' (the dK/dV kernel's sign convention)
-  const float qscale = -(p.scale * *p.n_ptr * *p.b_ptr);
-  if (qrow < N) {
-    T* dqg = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + qrow * p.dq.ss;
-#pragma unroll
-    for (int db = 0; db < ND32; ++db) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        v4 o4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = static_cast<T>(dq[db][4 * g + e] * qscale);
-        *reinterpret_cast<v4*>(dqg + db * 32 + g * 8 + 4 * hh) = o4;
-      }
-    }
-  }
+  // dQ rows through this wave's own dS' slots (its loads have all landed and
+  // no other wave reads them): rows 0-15 in the slot of stage 0, rows 16-31 in
+  // that of stage 1 (16 rows of D bf16 fill at most one 4 KB slot).
+  static_assert(16 * D * 2 <= 4096, "16 dQ rows per dS' slot");
+  T* dq0 = static_cast<T*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh;
+  store_rows_via_lds<T, D>(
+      dq, qscale, [&](int r) { return lds_ds + (r >> 4) * DSTAGE + wave * 4096 + (r & 15) * (D * 2); },
+      dq0 + static_cast<int64_t>(min(wq0, N - 1)) * p.dq.ss, p.dq.ss, N - wq0, lane);
 }
 
 // ---------------------------------------------------------------------------

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(fwd_threads<D>()) void ssa_fwd_f32_kernel(FwdParams
   const float* kg = static_cast<const float*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
   const float* vg = static_cast<const float*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
   float* og = static_cast<float*>(const_cast<void*>(p.o.ptr)) + sv.off(p.o, b) + h * p.o.sh;
-  const float n = *p.n_ptr, c = p.scale * *p.b_ptr;
+  const float n = *p.n_ptr, bv = *p.b_ptr, c = p.scale * bv;
 
   f32x4 qv[CP], acc[CP];
 #pragma unroll
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(bwd_threads<D>()) void ssa_bwd_dkdv_f32_kernel(BwdP
     vh[c4] = key < N ? ld4(vg + key * p.v.ss + col) : f32x4{0.f, 0.f, 0.f, 0.f};
     dkh[c4] = dvh[c4] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const float n = *p.n_ptr, c = p.scale * *p.b_ptr;
+  const float n = *p.n_ptr, bv = *p.b_ptr, c = p.scale * bv;
   float dn_acc = 0.f, dn_c = 0.f, db_acc = 0.f, db_c = 0.f;  // Kahan sums (lanes with part == 0)
   const int qstart = CAUSAL ? kb * kF32Pair : 0;
   for (int g = 0; g < G; ++g) {
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(bwd_threads<D>()) void ssa_bwd_dkdv_f32_kernel(BwdP
     }
   }
   if (key < N) {
-    const float ks_ = p.scale * n * *p.b_ptr;
+    const float ks_ = p.scale * n * bv;
     float* dkr = static_cast<float*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh + key * p.dk.ss;
     float* dvr = static_cast<float*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh + key * p.dv.ss;
 #pragma unroll
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(bwd_threads<D>()) void ssa_bwd_dq_f32_kernel(BwdPar
   }
   const int64_t mr = sv.mrow(b, h, p.Hq, p.T, p.N);
   const float mi = i < N ? p.m[mr + i] : 0.f, di = i < N ? p.delta[mr + i] : 0.f;
-  const float n = *p.n_ptr, c = p.scale * *p.b_ptr;
+  const float n = *p.n_ptr, bv = *p.b_ptr, c = p.scale * bv;
   const int kv_end = CAUSAL ? min(N, q0 + kF32Pair) : N;
   for (int k0 = 0; k0 < kv_end; k0 += kF32Tile) {
     __syncthreads();
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(bwd_threads<D>()) void ssa_bwd_dq_f32_kernel(BwdPar
     }
   }
   if (i < N) {
-    const float qs_ = p.scale * n * *p.b_ptr;
+    const float qs_ = p.scale * n * bv;
     float* dqr = static_cast<float*>(const_cast<void*>(p.dq.ptr)) + sv.off(p.dq, b) + h * p.dq.sh + i * p.dq.ss;
 #pragma unroll
     for (int c4 = 0; c4 < CP; ++c4) st4(dqr + 4 * (part * CP + c4), dqh[c4] * qs_);

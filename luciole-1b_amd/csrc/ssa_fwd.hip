@@ -427,20 +427,15 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
   const float l_tot = pair_sum(l_run);
   const float l_safe = l_tot > 0.f ? l_tot : 1.f;
   const float inv = 1.f / l_safe;
-  if (qrow < N) {
-#pragma unroll
-    for (int db = 0; db < ND32; ++db) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = db * 32 + g * 8 + 4 * hh;
-        typedef T t4 __attribute__((ext_vector_type(4)));
-        t4 o4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = static_cast<T>(acc[db][4 * g + e] * inv);
-        *reinterpret_cast<t4*>(og + qrow * p.o.ss + d0) = o4;
-      }
-    }
-    if (hh == 0) p.m[sv.mrow(b, h, p.Hq, p.T, p.N) + qrow] = m_run + log2f(l_safe);
+  // O rows through LDS (whole rows per store instruction): every wave is
+  // past its last read of the K/V ring, which then holds 32 rows of 2 D bytes
+  // per wave.
+  __syncthreads();
+  if (wq0 < N) {
+    store_rows_via_lds<T, D>(
+        acc, inv, [&](int r) { return lds0 + wave * (32 * D * 2) + r * (D * 2); },
+        og + static_cast<int64_t>(wq0) * p.o.ss, p.o.ss, N - wq0, lane);
+    if (qrow < N && hh == 0) p.m[sv.mrow(b, h, p.Hq, p.T, p.N) + qrow] = m_run + log2f(l_safe);
   }
 }
 
