@@ -147,10 +147,11 @@ __device__ __forceinline__ void store_key_block(const f32x16* acc, float scale, 
     if (okey < N) *reinterpret_cast<v4*>(row + 8 * i) = r;
   }
 }
-// Byte size of one wave's tile for store_key_block.
+// Byte size of one wave's LDS scratch for its dK / dV rows: the [d][key]
+// tile above, or 32 whole key rows (store_cols_via_lds, ssa_tile.hpp).
 template <int D>
 constexpr int key_block_tile_bytes() {
-  return D * 72;
+  return D * 72 > 32 * D * 2 ? D * 72 : 32 * D * 2;
 }
 
 // OFF32: every Q / dO row a workgroup reads lies below 2 GiB of its base
@@ -657,8 +658,18 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     const uint32_t tile = lds0 + wave * key_block_tile_bytes<D>();
     T* dkr = static_cast<T*>(const_cast<void*>(p.dk.ptr)) + sv.off(p.dk, b) + hk * p.dk.sh;
     T* dvr = static_cast<T*>(const_cast<void*>(p.dv.ptr)) + sv.off(p.dv, b) + hk * p.dv.sh;
-    store_key_block<T, D>(dk, -(p.scale * n * bv), dkr, p.dk.ss, k0w, N, tile, lane);
-    store_key_block<T, D>(dv, 1.f, dvr, p.dv.ss, k0w, N, tile, lane);
+    if constexpr (D >= 128) {
+      // whole key rows per store instruction through the wave's scratch (at
+      // D = 128 the kernel runs one wave per SIMD with registers to spare;
+      // below, the staging code's registers would cost the second wave)
+      auto slot = [&](int r) { return tile + r * (D * 2); };
+      const int64_t k0r = static_cast<int64_t>(min(k0w, N - 1));
+      store_cols_via_lds<T, D>(dk, -(p.scale * n * bv), slot, dkr + k0r * p.dk.ss, p.dk.ss, N - k0w, lane);
+      store_cols_via_lds<T, D>(dv, 1.f, slot, dvr + k0r * p.dv.ss, p.dv.ss, N - k0w, lane);
+    } else {
+      store_key_block<T, D>(dk, -(p.scale * n * bv), dkr, p.dk.ss, k0w, N, tile, lane);
+      store_key_block<T, D>(dv, 1.f, dvr, p.dv.ss, k0w, N, tile, lane);
+    }
   }
 
   // dn / db partial of this workgroup: lane butterfly, then waves in order.

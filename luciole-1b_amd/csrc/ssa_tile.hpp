@@ -412,41 +412,72 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
 }
 
-// Store one wave's 32 x D output block (rows row0 .. row0 + 31 of a [*, D]
-// bf16/fp16 matrix, row stride ss elements, rows >= nrows skipped) from MFMA
-// accumulators in the transposed layout -- lane (l32, hh) holds row l32,
-// elements 32 db + 8 g + 4 hh + (0..3) in acc[db][4 g ..] -- scaled by
-// `scale`.  Written straight from that layout every store instruction would
-// touch 32 rows with 16 bytes each; here the block goes through the wave's own
-// LDS scratch (`slot(r)`: byte address of row r, 2 D bytes per row, not used
-// by any other wave meanwhile) and comes back as whole rows, 16 lanes per row,
-// 16 bytes per lane.  16-byte chunks are XOR-swizzled by the row so that the
-// 8-byte writes spread over the banks.  The same wave writes and reads its
-// scratch, and LDS serves one wave's accesses in order.
+// A wave's 32 x D output block (rows row0 .. row0 + 31 of a [*, D] bf16/fp16
+// matrix, row stride ss elements, rows >= nrows skipped) leaves the matrix
+// core in a transposed register layout, so a direct store instruction would
+// touch 32 rows with 8-16 bytes each.  These helpers stage the block in the
+// wave's own LDS scratch (`slot(r)`: byte address of row r, 2 D bytes per row,
+// used by no other wave meanwhile) and store it as whole rows: 16 lanes per
+// row, 16 bytes per lane.  Within a row the 16-byte chunks are XOR-swizzled by
+// the row index, which spreads the staging writes over the banks.  The wave
+// writes and reads its scratch itself, and LDS serves one wave in order.
+
+// LDS byte offset of element d within row r of the staging layout.
+template <int D>
+__device__ __forceinline__ uint32_t stage_off(int r, int d) {
+  constexpr int CH = D * 2 / 16;  // 16-byte chunks per row
+  return static_cast<uint32_t>((((d >> 3) ^ (r & (CH - 1))) << 4) + ((d & 7) << 1));
+}
+
+// Staged rows to global memory, whole rows per store instruction.
+template <typename T, int D, typename SlotFn>
+__device__ __forceinline__ void stage_to_rows(SlotFn slot, T* row0, int64_t ss, int nrows, int lane) {
+  constexpr int CH = D * 2 / 16;
+#pragma unroll
+  for (int k = 0; k < CH / 2; ++k) {
+    const int q = 64 * k + lane, r = q / CH, c = q % CH;
+    const u32x4 v = *(__attribute__((address_space(3))) u32x4*)(uintptr_t)(slot(r) + stage_off<D>(r, 8 * c));
+    if (r < nrows) *reinterpret_cast<u32x4*>(row0 + static_cast<int64_t>(r) * ss + c * 8) = v;
+  }
+}
+
+// Row-per-lane accumulators: lane (l32, hh) holds row l32, elements
+// 32 db + 8 g + 4 hh + (0..3) in acc[db][4 g ..] (the forward's O, dQ).
 template <typename T, int D, typename SlotFn>
 __device__ __forceinline__ void store_rows_via_lds(const f32x16* acc, float scale, SlotFn slot, T* row0, int64_t ss,
                                                    int nrows, int lane) {
   typedef T v4 __attribute__((ext_vector_type(4)));
-  constexpr int ND32 = D / 32, CH = D * 2 / 16;  // 16-byte chunks per row
   const int l32 = lane & 31, hh = lane >> 5;
   const uint32_t wr = slot(l32);
 #pragma unroll
-  for (int db = 0; db < ND32; ++db) {
+  for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       v4 o4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o4[e] = static_cast<T>(acc[db][4 * g + e] * scale);
-      const int ch = (4 * db + g) ^ (l32 & (CH - 1));
-      *(__attribute__((address_space(3))) v4*)(uintptr_t)(wr + ch * 16 + 8 * hh) = o4;
+      *(__attribute__((address_space(3))) v4*)(uintptr_t)(wr + stage_off<D>(l32, 32 * db + 8 * g + 4 * hh)) = o4;
     }
   }
+  stage_to_rows<T, D>(slot, row0, ss, nrows, lane);
+}
+
+// Column-per-lane accumulators: lane (l32, hh) holds element 32 db + l32 of
+// rows crow(r, hh), r = 0..15, in acc[db][r] (dK, dV).
+template <typename T, int D, typename SlotFn>
+__device__ __forceinline__ void store_cols_via_lds(const f32x16* acc, float scale, SlotFn slot, T* row0, int64_t ss,
+                                                   int nrows, int lane) {
+  const int l32 = lane & 31, hh = lane >> 5;
 #pragma unroll
-  for (int k = 0; k < CH / 2; ++k) {
-    const int q = 64 * k + lane, r = q / CH, c = q % CH;
-    const u32x4 v = *(__attribute__((address_space(3))) u32x4*)(uintptr_t)(slot(r) + (c ^ (r & (CH - 1))) * 16);
-    if (r < nrows) *reinterpret_cast<u32x4*>(row0 + static_cast<int64_t>(r) * ss + c * 8) = v;
+  for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = crow(r, hh);
+      *(__attribute__((address_space(3))) T*)(uintptr_t)(slot(row) + stage_off<D>(row, 32 * db + l32)) =
+          static_cast<T>(acc[db][r] * scale);
+    }
   }
+  stage_to_rows<T, D>(slot, row0, ss, nrows, lane);
 }
 
 }  // namespace ssa
