@@ -578,10 +578,11 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
     // TK ticks per slot; tick t issues the MFMAs G in [t NG / TK, (t + 1) NG /
     // TK), each after the operand read two MFMAs ahead, beside four
     // independent stages on EPT elements each: A(t + 2), B(t + 1), C1(t),
-    // C2(t - 1) in units of EPT elements.  Sixteen ticks at D = 128 (two
-    // MFMAs per tick), eight below (a tick carries more element work where
-    // the MFMAs are fewer).
-    constexpr int TK = D >= 128 ? 16 : 8, EPT = 16 / TK;
+    // C2(t - 1) in units of EPT elements.  Sixteen ticks at D >= 64 (two
+    // MFMAs per tick at D = 128, one at D = 64: at D = 64 the shorter live
+    // ranges of one element per stage keep every causal instance within 256
+    // registers, two waves per SIMD), eight at D = 32.
+    constexpr int TK = D >= 64 ? 16 : 8, EPT = 16 / TK;
     auto tick = [&](auto tc) {
       constexpr int t = decltype(tc)::value;
       constexpr int G0 = t * NG / TK, G1 = (t + 1) * NG / TK;
