@@ -42,6 +42,7 @@ HIPCC_FLAGS = [
 # AGPRs by the inline assembly of ssa_common.hpp (mfma32_acc / acc_fence).
 SOURCE_FLAGS = {
     "ssa_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "ssa_bwd_dkdv2w.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

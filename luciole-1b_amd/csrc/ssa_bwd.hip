@@ -17,6 +17,8 @@
 //   dV_j += P dO_i,  dK_j += scale n b dS' q_i,  dQ_i += scale n b dS' k_j
 //   dn  += ln2 * dT sL,  db += n scale dS' (q_i.k_j)
 // The constant factors (scale n b, ln2, n scale) are applied once at the end.
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "ssa_common.hpp"
@@ -1072,10 +1074,19 @@ static bool dkdv_off32(const BwdParams& p, int D, bool causal) {
   return p.ds == nullptr || G * ds_tiles_per_head(p.N, causal) * 1024 < lim;
 }
 
+// SSA_DKDV2W=1 selects the two-waves-per-SIMD dK/dV kernel
+// (ssa_bwd_dkdv2w.hip) for bf16 / fp16; read at every launch, so a caller
+// can switch between the two kernels within one process.
+static bool use_dkdv2w() {
+  const char* e = getenv("SSA_DKDV2W");
+  return e != nullptr && e[0] == '1';
+}
+
 template <typename T, int D, bool CAUSAL>
 static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
   const int grid = dkdv_key_blocks(p.N) * p.B * p.Hkv;
   const bool o32 = dkdv_off32(p, D, CAUSAL);
+  if (use_dkdv2w()) return launch_bwd_dkdv2w(p, std::is_same_v<T, __bf16> ? 0 : 1, D, CAUSAL, o32, s);
   if (p.ds != nullptr) {
     if (o32)
       hipLaunchKernelGGL((ssa_bwd_dkdv_kernel<T, D, CAUSAL, true, true>), dim3(grid), dim3(256), 0, s, p);

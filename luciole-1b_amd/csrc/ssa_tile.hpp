@@ -57,6 +57,16 @@ struct LoadLane {
     hoff = static_cast<uint32_t>(half * 16);
     off = static_cast<uint32_t>(r * ss * 2) + hoff;
   }
+  // The Swz8 layout (Swz8Tile below): row r of chunk c at position
+  // r ^ 8 (c & 1).  A 1 KB piece covers chunks 2 cp and 2 cp + 1, so the
+  // row a lane fetches depends on its half only, not on the wave.
+  struct Swz8 {};
+  __device__ __forceinline__ LoadLane(int lane, int64_t ss, Swz8) {
+    const int pos = lane & 31, half = lane >> 5;
+    r = pos ^ (8 * half);
+    hoff = static_cast<uint32_t>(half * 16);
+    off = static_cast<uint32_t>(r * ss * 2) + hoff;
+  }
 };
 
 // Issue the loads of one ROWS x D tile (rows row0.. of a [*, D] matrix with
@@ -429,12 +439,13 @@ __device__ __forceinline__ uint32_t stage_off(int r, int d) {
   return static_cast<uint32_t>((((d >> 3) ^ (r & (CH - 1))) << 4) + ((d & 7) << 1));
 }
 
-// Staged rows to global memory, whole rows per store instruction.
-template <typename T, int D, typename SlotFn>
+// Staged rows (ROWS of them) to global memory, whole rows per store instruction.
+template <typename T, int D, int ROWS = 32, typename SlotFn>
 __device__ __forceinline__ void stage_to_rows(SlotFn slot, T* row0, int64_t ss, int nrows, int lane) {
   constexpr int CH = D * 2 / 16;
+  static_assert(ROWS * CH % 64 == 0, "whole store instructions");
 #pragma unroll
-  for (int k = 0; k < CH / 2; ++k) {
+  for (int k = 0; k < ROWS * CH / 64; ++k) {
     const int q = 64 * k + lane, r = q / CH, c = q % CH;
     const u32x4 v = *(__attribute__((address_space(3))) u32x4*)(uintptr_t)(slot(r) + stage_off<D>(r, 8 * c));
     if (r < nrows) *reinterpret_cast<u32x4*>(row0 + static_cast<int64_t>(r) * ss + c * 8) = v;
