@@ -6,14 +6,20 @@ the result -- a complete set of heads, independent of every other slice --
 goes through the fp64 oracle (oracle/ssa_oracle.py): out and m against the
 exact forward, dq / dk / dv against the kernel-level backward (delta from the
 kernel's own out, as ssa_triton_kernel.py:291-294 defines it), to the bar of
-parity_util.  dn / db are sums over every head and are checked at full size
-only through the smaller parity tests.  The packed case checks one head of
-the 16,384-token stream.
+parity_util.  dn / db, sums over every pair of every head, are checked for the
+whole problem: the chunked fp64 oracle (ssa_forward_backward_chunked, the
+kernel-level backward of the kernel's own out) runs on every (batch, kv-head)
+slice in a thread pool and the slices' sums are added in a fixed order, to the
+scalar bar of parity_util (2e-3 + 2e-2 |ref|, the reference's
+check_ssa_triton_parity.py:1060-1069).  The packed case checks one head of the
+16,384-token stream.
 """
 
 from __future__ import annotations
 
+import concurrent.futures as cf
 import math
+import os
 import sys
 
 import numpy as np
@@ -21,13 +27,38 @@ import pytest
 import torch
 
 from oracle import ssa_oracle as so
-from parity_util import assert_parity, compare, make_inputs
+from parity_util import assert_parity, compare, make_inputs, scalar_err
 
 pytestmark = pytest.mark.gpu
 
 
 def _np64(t):
     return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def whole_dn_db(q, k, v, do, out, scale, n_val, b_val, causal=True):
+    """dn, db of the whole problem from the chunked fp64 oracle: one task per
+    (batch, kv-head) slice (a complete set of heads), run in threads (NumPy
+    releases the GIL in its array loops; BLAS is held to one thread per call so
+    the threads do not oversubscribe the cores), summed in slice order."""
+    from threadpoolctl import threadpool_limits
+
+    B, Hq, Hkv = q.shape[0], q.shape[1], k.shape[1]
+    G = Hq // Hkv
+    qn, kn, vn, don, on = (_np64(t) for t in (q, k, v, do, out))
+
+    def one(bh):
+        bi, hk = bh
+        hs = slice(hk * G, (hk + 1) * G)
+        r = so.ssa_forward_backward_chunked(qn[bi:bi + 1, hs], kn[bi:bi + 1, hk:hk + 1], vn[bi:bi + 1, hk:hk + 1],
+                                            don[bi:bi + 1, hs], scale, n_val, b_val, causal,
+                                            out_for_delta=on[bi:bi + 1, hs])
+        return r["dn"], r["db"]
+
+    slices = [(bi, hk) for bi in range(B) for hk in range(Hkv)]
+    with threadpool_limits(limits=1), cf.ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        parts = list(ex.map(one, slices))
+    return sum(p[0] for p in parts), sum(p[1] for p in parts)
 
 
 DENSE = [
@@ -52,6 +83,11 @@ def test_fullsize_slice_matches_oracle(gpu, name, B, Hq, Hkv, N, D, sl):
     dq, dk, dv, dn, db = ssa_flash_attn_backward(q, k, v, out, do, m, scale, n, b, causal=True)
     torch.cuda.synchronize()
     assert torch.isfinite(dn) and torch.isfinite(db)
+    ref_dn, ref_db = whole_dn_db(q, k, v, do, out, scale, n_val, b_val)
+    sres = {"dn": scalar_err(dn.item(), ref_dn), "db": scalar_err(db.item(), ref_db)}
+    print(f"[gpu result] {label}: whole-problem dn {dn.item():.6e} vs {ref_dn:.6e} (rel {sres['dn']['rel']:.1e}), "
+          f"db {db.item():.6e} vs {ref_db:.6e} (rel {sres['db']['rel']:.1e})", file=sys.stderr, flush=True)
+    assert_parity(sres, label + " [whole-problem dn / db]")
 
     bi, hk = sl
     G = Hq // Hkv
@@ -105,3 +141,22 @@ def test_fullsize_varlen_head_matches_oracle(gpu):
     assert merr < 1e-2, f"{label}: m {merr}"
     assert_parity(res, label)
     assert_parity(res_k, label + " [kernel-level]")
+
+    # dn / db of the whole stream: every head through the oracle (threads), summed in head order
+    from threadpoolctl import threadpool_limits
+
+    qn, kn, vn, don, on = (_np64(t) for t in (q, k, v, do, out))
+    cun = cu_host.numpy()
+
+    def head(hh):
+        r = so.ssa_varlen_forward_backward(qn[:, hh:hh + 1], kn[:, hh:hh + 1], vn[:, hh:hh + 1], don[:, hh:hh + 1],
+                                           cun, scale, n_val, b_val, True, out_for_delta=on[:, hh:hh + 1])
+        return r["dn"], r["db"]
+
+    with threadpool_limits(limits=1), cf.ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        parts = list(ex.map(head, range(H)))
+    ref_dn, ref_db = sum(p_[0] for p_ in parts), sum(p_[1] for p_ in parts)
+    sres = {"dn": scalar_err(dn.item(), ref_dn), "db": scalar_err(db.item(), ref_db)}
+    print(f"[gpu result] {label}: whole-stream dn rel {sres['dn']['rel']:.1e}, db rel {sres['db']['rel']:.1e}",
+          file=sys.stderr, flush=True)
+    assert_parity(sres, label + " [whole-stream dn / db]")

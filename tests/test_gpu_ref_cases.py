@@ -11,6 +11,10 @@ ours.  The inputs are not the reference's (its CUDA RNG stream is not
 reproducible here), so the comparison is of error levels, not of values.
 
     python tests/test_gpu_ref_cases.py REPORT.md   # writes the side-by-side table
+
+and, beside it, REPORT.json: every case's errors, the limits they are held to
+and a pass flag per case, as the reference harness's JSON report
+(check_ssa_triton_parity.py:1118-1137).
 """
 
 from __future__ import annotations
@@ -57,14 +61,41 @@ def test_reference_case(gpu, idx):
     _check(label, res_exact, res_kernel, mres)
 
 
+_KEEP = ("max_abs_vs_rounded", "within_bound", "allclose", "got", "ref", "rel")
+
+
+def _plain(st):
+    """The report fields of a result dict: flags as they are, numbers to 3 significant digits."""
+    out = {}
+    for k, v in st.items():
+        if k not in _KEEP:
+            continue
+        v = v.item() if hasattr(v, "item") else v
+        out[k] = v if isinstance(v, bool) else float(f"{v:.3g}")
+    return out
+
+
 def main(path):
+    import parity_util as pu
+
     dev = torch.device("cuda:0")
     rows = []
+    report = []
     worst = {t: [0.0, 0.0] for t in ("out", "dq", "dk", "dv")}
     worst_s = {t: [0.0, 0.0] for t in ("dn", "db")}
     for idx, entry in enumerate(CASES):
         label, res_exact, res_kernel, mres = _run_case(dev, entry, 1234 + idx)
         ref = entry["v4_vs_ref"]
+        try:
+            _check(label, res_exact, res_kernel, mres)
+            passed, err = True, None
+        except AssertionError as e:
+            passed, err = False, str(e)
+        report.append({"case": entry["case"], "seed": 1234 + idx, "passed": passed, "error": err, "m_max_abs": mres,
+                       "ours_vs_exact": {t: _plain(v) for t, v in res_exact.items()},
+                       "ours_kernel_level": {t: _plain(v) for t, v in res_kernel.items()},
+                       "reference_recorded": {t: float(f"{ref[t]['max_abs']:.3g}") for t in ("out", "dq", "dk", "dv")}
+                       | {t: float(f"{ref[t]['abs_diff'] / max(abs(ref[t]['ref']), 1e-12):.3g}") for t in ("dn", "db")}})
         row = [_case_id(entry)]
         for t in ("out", "dq", "dk", "dv"):
             ours = res_exact[t]["max_abs_vs_rounded"]
@@ -82,9 +113,28 @@ def main(path):
     lines.append("| **max over cases** | " + " | ".join(f"**{a:.2e} / {b:.2e}**" for a, b in worst.values())
                  + " | " + " | ".join(f"**{a:.1e} / {b:.1e}**" for a, b in worst_s.values()) + " |")
     lines += ["| " + " | ".join(r) + " |" for r in rows]
-    Path(path).write_text("Each cell: this build (MI355X) / reference Triton kernel (A100, recorded); "
-                          "max |x - fp32 oracle rounded to the input dtype|.\n\n" + "\n".join(lines) + "\n")
-    print(f"wrote {path}")
+    ok = all(r["passed"] for r in report)
+    Path(path).write_text(
+        "# Parity on the reference harness's 96 kernel case shapes: this build vs the reference Triton kernel\n\n"
+        f"Command (repo root, GPU box): `python tests/test_gpu_ref_cases.py {path}`, which also writes\n"
+        f"`{Path(path).with_suffix('.json')}` (per case: the shape, seed, pass flag, this build's errors against the "
+        "fp64\noracle and the kernel-level backward, the reference's recorded errors; the limits at the top).\n"
+        f"{'All' if ok else 'NOT all'} {len(report)} cases pass (`overall_passed: {str(ok).lower()}`).  Inputs are "
+        "seeded here (the reference's CUDA RNG stream is not\nreproducible), so the comparison is of error levels on "
+        "the same shapes, not of values.\n\n"
+        "Each cell: this build (MI355X) / reference Triton kernel (A100, recorded); "
+        "max |x - fp32 oracle rounded to the input dtype|.\n\n" + "\n".join(lines) + "\n")
+    meta = {"device": torch.cuda.get_device_name(dev), "torch": torch.__version__, "hip": torch.version.hip,
+            "source": "tests/test_gpu_ref_cases.py; reference levels from tests/golden/ref_parity_levels.json"}
+    limits = {"tensor_atol": pu.ATOL, "tensor_rtol": pu.RTOL, "scalar_atol": pu.SCALAR_ATOL,
+              "scalar_rtol": pu.SCALAR_RTOL, "elementwise": "max(2e-2, 1 ulp of the output dtype at |ref|)",
+              "m_max_abs": 1e-2}
+    out = {"meta": meta, "limits": limits, "cases": report, "overall_passed": all(r["passed"] for r in report)}
+    # one line per case
+    cases = ",\n".join(json.dumps(c, separators=(",", ":")) for c in out.pop("cases"))
+    head = json.dumps(out, indent=1)[:-2]
+    Path(path).with_suffix(".json").write_text(head + ',\n "cases": [\n' + cases + "\n ]\n}\n")
+    print(f"wrote {path} and {Path(path).with_suffix('.json')}")
 
 
 if __name__ == "__main__":

@@ -22,7 +22,8 @@ ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "luciole-1b_amd" / "csrc"
 BUILD = ROOT / "luciole-1b_amd" / "_build"
 SANITIZED = ("ssa_abi", "ssa_noalloc", "decoder_ops")
-PLAIN = ("ssa_bwd", "ssa_decode", "ssa_f32", "ssa_fwd", "ssa_varlen_fill")
+# every other source of the library, linked as built
+PLAIN = tuple(sorted(f.stem for f in CSRC.glob("*.hip") if f.stem not in SANITIZED))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CLANG = "/opt/rocm/llvm/bin/clang"
 HOST_SAN = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
