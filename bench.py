@@ -45,7 +45,10 @@ for _p in (str(ROOT), str(ROOT / "luciole-1b_amd")):
 # MI355X published dense peaks.
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (2.5 PFLOP/s class)
 PEAK_HBM_GBPS = 8000.0
-PEAK_FP32_TFLOPS = 157.3   # MI355X fp32, vector ALU and dense matrix alike
+PEAK_FP32_TFLOPS = 157.3   # MI355X published fp32 peak (packed fp32 VALU or fp32 MFMA)
+# fp32 FMA on the vector ALU without packed forms (which this build leaves out):
+# 256 CU x 4 SIMD x 16 lanes x 2 FLOP x 2.4 GHz
+PEAK_FP32_VALU_TFLOPS = 78.6
 
 CONFIGS = {
     # name: (B, Hq, Hkv, S, D, causal)
@@ -232,15 +235,33 @@ def measured_counters(config):
     keys = ("counter_ms", "clock_ghz", "mfma_busy", "valu_busy", "valu_per_mfma", "trans_per_mfma",
             "salu_per_mfma", "lds_per_mfma", "issue", "wait_any", "wait_dep", "lds_fifo_full")
     out = {}
-    for line in f.read_text().splitlines():
+    text = f.read_text()
+    # "Library: built from commit <sha>" in the profile names the kernels it measured
+    mb = re.search(r"built from commit (\w+)", text)
+    for line in text.splitlines():
         m = COUNTER_ROW.match(line)
         if m:
             vals = [float(x) for x in m.groups()[1:]]
             d = dict(zip(keys, vals))
             for k in ("mfma_busy", "valu_busy", "issue", "wait_any", "wait_dep", "lds_fifo_full"):
                 d[k] /= 100.0
+            d["build"] = mb.group(1) if mb else None
             out[m.group(1)] = d
     return out
+
+
+def limiter_from_counters(cn):
+    """What the counter row says holds a kernel below its compute roof: a unit
+    busy >= 80 % of the SIMD-cycles is saturated; otherwise the waves' waiting
+    share decides between latency (>= 35 % of wave time waiting) and issue."""
+    mf, va, wait = cn["mfma_busy"], cn["valu_busy"], cn["wait_any"] + cn["wait_dep"]
+    if mf >= 0.8:
+        return f"matrix core saturated ({mf:.0%} busy)"
+    if va >= 0.8:
+        return f"vector ALU saturated ({va:.0%} busy)"
+    what = (f"matrix core {mf:.0%} and VALU {va:.0%} busy; waves issue {cn['issue']:.0%} of their time and wait "
+            f"{wait:.0%} ({cn['wait_any']:.0%} on counters and barriers, {cn['wait_dep']:.0%} on dependencies)")
+    return ("latency: " if wait >= 0.35 else "issue: ") + what
 
 
 def pairs_dense(B, Hq, S, causal):
@@ -469,24 +490,40 @@ def main():
         kernels["ssa_bwd_dq_kernel"]["alg_bytes"] = ds_bytes + (B * Hkv + B * Hq) * S * D * esize
     pre_bytes = 2 * B * Hq * S * D * esize + 4 * B * Hq * S
     kernels["ssa_bwd_preprocess_kernel"]["alg_bytes"] = pre_bytes
-    # fp32 runs on the vector ALU (MI355X fp32: 157.3 TFLOP/s, vector and matrix alike)
+    # fp32 inputs run on the vector ALU: priced against the published fp32 peak
+    # (157.3, which needs packed fp32) and, as frac_valu_peak, against what
+    # non-packed fp32 FMAs can reach (78.6)
     peak_flops = PEAK_FP32_TFLOPS if dtype == torch.float32 else PEAK_BF16_TFLOPS
-    for name, kd in kernels.items():
-        if "alg_flop" in kd:
-            kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
-            kd["frac_peak"] = kd["tflops"] / peak_flops
-            kd["bound"] = "valu" if dtype == torch.float32 else "mfma"
-        if "alg_bytes" in kd:
-            kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
-            kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
-            kd["bound"] = "hbm"
     traffic = measured_traffic(args.config) if args.dtype == "bf16" else {}
     counters = measured_counters(args.config) if args.dtype == "bf16" else {}
     hip_name = {"ssa_bwd_dq_kernel": "ssa_bwd_dq_ds_kernel" if ds_bytes else "ssa_bwd_dq_kernel",
                 "ssa_bwd_reduce_kernel": "ssa_reduce_partials_kernel"}
+    # algorithmic HBM bytes of the FLOP-priced kernels (inputs read once, outputs written once)
+    tq, tkv, rows_b = B * Hq * S * D * esize, B * Hkv * S * D * esize, B * Hq * S * 4
+    alg_io = {"ssa_fwd_kernel": 2 * tq + 2 * tkv + rows_b,
+              "ssa_bwd_dkdv_kernel": 2 * tq + 4 * tkv + 2 * rows_b + ds_bytes}
+    ridge = peak_flops * 1e12 / (PEAK_HBM_GBPS * 1e9)  # FLOP per HBM byte where the two roofs meet
     for name, kd in kernels.items():
         kd["hbm_bytes"] = traffic.get(name)
         kd["counters"] = counters.get(hip_name.get(name, name))
+        if "alg_flop" in kd:
+            kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
+            kd["frac_peak"] = kd["tflops"] / peak_flops
+            if dtype == torch.float32:
+                kd["frac_valu_peak"] = kd["tflops"] / PEAK_FP32_VALU_TFLOPS
+            # the roof that bounds it: compute when its intensity (FLOP per HBM
+            # byte, measured traffic where a profile exists) is above the ridge
+            nbytes = kd["hbm_bytes"] or alg_io.get(name)
+            if nbytes:
+                kd["intensity_flop_per_byte"] = kd["alg_flop"] / nbytes
+                compute = kd["intensity_flop_per_byte"] > ridge
+            else:
+                compute = True
+            kd["bound"] = ("valu" if dtype == torch.float32 else "mfma") if compute else "hbm"
+        if "alg_bytes" in kd:
+            kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
+            kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
+            kd["bound"] = "hbm"
     dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
     kd = kernels[dominant]
     if kd.get("bound") in ("mfma", "valu"):
@@ -503,10 +540,8 @@ def main():
                 "mfma_busy": cn["mfma_busy"], "valu_busy": cn["valu_busy"],
                 "valu_per_mfma": cn["valu_per_mfma"], "trans_per_mfma": cn["trans_per_mfma"],
                 "salu_per_mfma": cn["salu_per_mfma"], "wait_frac": cn["wait_any"] + cn["wait_dep"],
-                "clock_ghz": cn["clock_ghz"],
-                "limiter": "issue and latency: neither the matrix core nor the VALU is saturated; the waves "
-                           "wait on operand reads, dependencies and the per-step barrier",
-                "source": f"profiles/ssa_counters_{args.config}.md"}
+                "clock_ghz": cn["clock_ghz"], "limiter": limiter_from_counters(cn),
+                "source": f"profiles/ssa_counters_{args.config}.md", "profile_build": cn.get("build")}
     else:
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": kd["gbps"], "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": kd["hbm_bytes"],

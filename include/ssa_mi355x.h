@@ -190,7 +190,10 @@ int32_t ssa_bwd_reduce(const ssa_bwd_args* args, void* stream);
  * about 1 MiB); larger problems return SSA_ERR_SCRATCH with nothing
  * launched.  Calls no allocating routine.  Every call on a device shares that
  * device's array: calls in flight at the same time on one device (on
- * different streams) race; calls in stream order do not.
+ * different streams) race; calls in stream order do not.  The first call on
+ * each device looks the array's address up (hipGetSymbolAddress): make it
+ * outside graph capture; later calls may be captured (they launch kernels
+ * only, no memset or copy nodes).
  */
 #define SSA_NOALLOC_SCRATCH_BYTES (16ll << 20)
 int32_t ssa_bwd_noalloc(const ssa_bwd_args* args, void* stream);

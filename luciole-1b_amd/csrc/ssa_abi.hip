@@ -201,7 +201,10 @@ const char* ssa_status_string(int32_t status) {
   switch (status) {
     case SSA_OK: return "ok";
     case SSA_ERR_NULL_POINTER: return "a required pointer is NULL";
-    case SSA_ERR_SHAPE: return "invalid shape (batch/heads/seqlen must be > 0 and Hq % Hkv == 0)";
+    case SSA_ERR_SHAPE:
+      return "invalid shape (batch, heads, seqlen must be > 0 and Hq % Hkv == 0; size limits: seqlen and decode "
+             "capacity <= 2^30, batch * heads_q * ceil(seqlen / 128) <= 2^28, at most 2^31 - 1 query rows per "
+             "launch: batch * heads_q * seqlen, or heads_q * total_tokens for packed sequences)";
     case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128; fp32 also 16)";
     case SSA_ERR_DTYPE: return "unsupported dtype (supported: bf16, fp16, fp32; the decode step bf16, fp16)";
     case SSA_ERR_ALIGNMENT:

@@ -82,6 +82,10 @@ def test_ds_workspace_bytes(N, causal):
 def test_ds_workspace_bytes_headline_and_empty():
     lib = _lib.lib()
     assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 4096, 1) == 4 * 16 * 128 * 129 * 1024
+    # the status text names the size limits a caller may have hit
+    text = _lib.status_text(_lib.SSA_ERR_SHAPE)
+    for limit in ("2^30", "2^28", "2^31 - 1", "query rows"):
+        assert limit in text, (limit, text)
     assert lib.ssa_bwd_ds_workspace_bytes(0, 16, 4096, 1) == 0
     assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 0, 0) == 0
 
@@ -178,6 +182,10 @@ def test_size_limits():
     assert lib.ssa_decode_num_splits(1, 8, 8, 2**31 - 1, 0) == 0
     assert lib.ssa_decode_num_splits(1, 8, 8, 4096, 2**31 - 1) == 32  # more splits than 128-key blocks: clamped
     assert lib.ssa_bwd_ds_workspace_bytes(4, 16, 4096, 1) == 4 * 16 * 128 * 129 * 1024
+    # the status text names the size limits a caller may have hit
+    text = _lib.status_text(_lib.SSA_ERR_SHAPE)
+    for limit in ("2^30", "2^28", "2^31 - 1", "query rows"):
+        assert limit in text, (limit, text)
 
 
 def test_fwd_null_args():
