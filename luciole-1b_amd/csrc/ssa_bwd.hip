@@ -23,6 +23,7 @@
 
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
+#include "ssa_plan.hpp"
 #include "ssa_tile.hpp"
 
 namespace ssa {
@@ -81,35 +82,7 @@ __global__ __launch_bounds__(256) void ssa_bwd_preprocess_kernel(BwdParams p) {
 // issues vector work.  Sub-tiles (Q, dO, M, Delta) live in four LDS buffers:
 // sub-tile t is loaded in slot t - 2 (its buffer last held t - 4, read for
 // the last time in slot t - 3) and complete at the start of slot t - 1.
-// Step st of a dK/dV workgroup -> (q-head g, sub-tile i), walked one step at a
-// time without divisions: masked sub-tiles of every q-head first (j < per_m:
-// i = j for the nlo diagonal ones, then the partial last sub-tile), then the
-// unmasked ones (i = nlo + j).  Scalar state.
-struct StepWalk {
-  int g, j;
-  bool unmasked;
-  __device__ __forceinline__ explicit StepWalk(int nmasked) : g(0), j(0), unmasked(nmasked == 0) {}
-  __device__ __forceinline__ void next(int per_m, int per_u, int G) {
-    ++j;
-    if (j >= (unmasked ? per_u : per_m)) {
-      j = 0;
-      if (++g >= G) {
-        g = 0;
-        unmasked = true;
-      }
-    }
-  }
-  __device__ __forceinline__ int sub(int nlo, int nsub) const { return unmasked ? nlo + j : (j < nlo ? j : nsub - 1); }
-  // The same two inside the unmasked steps (the fast slots walk only those;
-  // past the last step g runs to G, which no step reads).
-  __device__ __forceinline__ void next_unmasked(int per_u) {
-    if (++j >= per_u) {
-      j = 0;
-      ++g;
-    }
-  }
-  __device__ __forceinline__ int sub_unmasked(int nlo) const { return nlo + j; }
-};
+// The step order and walk: DkdvPlan / StepWalk (ssa_plan.hpp).
 
 // Store one wave's 32 keys x D block of dK or dV: the lane holds d = 32 db +
 // l32 of key rows k0w + crow(r, hh).  The block goes through the wave's own
@@ -164,27 +137,22 @@ template <typename T, int D, bool CAUSAL, bool DS, bool OFF32>
 __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
-  constexpr int BN = 128, BMQ = 32, NB = 4;
+  using Loads = DkdvLoads<D, CAUSAL, OFF32>;
+  using Plan = typename Loads::Plan;
+  constexpr int BMQ = Loads::BMQ;
   constexpr int ND16 = D / 16, ND32 = D / 32;
-  constexpr int TILE = BMQ * D * 2;    // one Q (or dO) sub-tile
-  constexpr int BUF = 2 * TILE + 256;  // Q, dO, M[32], Delta[32]
-  __shared__ __attribute__((aligned(1024))) char smem[NB * BUF];
+  constexpr int TILE = Loads::TILE;  // one Q (or dO) sub-tile
+  __shared__ __attribute__((aligned(1024))) char smem[Loads::LDS_BYTES];
   __shared__ float red[2][4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int nkb = dkdv_key_blocks(p.N);
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  // Logical order (kv-head, sequence), key blocks as in the forward's
-  // dispatch order (ascending = heaviest first under causal).
-  int bhk, kb;
-  dispatch_order(L, gridDim.x / nkb, nkb, p.cu_seqlens ? 1 : kOrderGroup, bhk, kb);
-  const int b = bhk % p.B, hk = bhk / p.B;
-  const int G = p.Hq / p.Hkv;
-  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
-  const int N = sv.N;
-  if (kb * BN >= N) {  // packed: past the end of a shorter document
+  // dispatch and step order (ssa_plan.hpp)
+  const Plan pl(p, blockIdx.x, gridDim.x);
+  const int nkb = pl.nkb, bhk = pl.bhk, kb = pl.kb, b = pl.b, hk = pl.hk, G = pl.G, N = pl.N;
+  const SeqView& sv = pl.sv;
+  if (pl.empty()) {  // packed: past the end of a shorter document
     if (tid == 0) {
       const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
       p.partials[static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
@@ -199,80 +167,28 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   const uint32_t lds0 = lds_addr(smem);
   const RowBase<D> rb(l32, hh);
   const TrBase<D> tb(lane);
-  const LoadLane llq(lane, wave, p.q.ss), lld(lane, wave, p.dout.ss);
 
-  const int k0 = kb * BN;
+  const int k0 = pl.k0;
   const int k0w = k0 + wave * 32;
   const int key = k0w + l32;
   const T* kg = static_cast<const T*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
   const T* vg = static_cast<const T*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
 
-  const int qstart = CAUSAL ? k0 : 0;
-  const int nsub = (N - qstart + BMQ - 1) / BMQ;
-  const int nsteps = G * nsub;
-  const bool key_edge = k0 + BN > N;
-  // Step order: every sub-tile that needs masks first (the causal diagonal,
-  // a partial last sub-tile, or all of them at the sequence end), then the
-  // unmasked ones.
-  const int nlo = key_edge ? nsub : (CAUSAL ? min(BN / BMQ, nsub) : 0);
-  const int ntail = (!key_edge && (N % BMQ) != 0 && nsub > nlo) ? 1 : 0;
-  const int per_m = nlo + ntail, per_u = nsub - per_m;  // per q-head
-  const int nmasked = G * per_m;
-  auto step_q0 = [&](int st, int& g) {
-    int i;
-    if (st < nmasked) {
-      g = st / per_m;
-      const int j = st - g * per_m;
-      i = j < nlo ? j : nsub - 1;
-    } else {
-      const int su = st - nmasked;
-      g = su / per_u;
-      i = nlo + (su - g * per_u);
-    }
-    return qstart + i * BMQ;
-  };
+  const int qstart = pl.qstart, nsub = pl.nsub, nsteps = pl.nsteps, nlo = pl.nlo;
+  const int per_m = pl.per_m, per_u = pl.per_u, nmasked = pl.nmasked;
+  auto step_q0 = [&](int st, int& g) { return pl.step_q0(st, g); };
   // a masked step whose queries all precede this wave's keys (or no keys)
-  auto skipped = [&](int st) {
-    int g;
-    return st < nmasked && (k0w >= N || (CAUSAL && step_q0(st, g) + BMQ - 1 < k0w));
-  };
-  auto bufof = [&](int st) { return lds0 + (st & (NB - 1)) * BUF; };
+  auto skipped = [&](int st) { return pl.skipped(st, k0w); };
+  auto bufof = [&](int st) { return Loads::buf(lds0, st); };
 
   // walkers at the next step to load (j + 2) and at the current step j
   StepWalk wi(nmasked), wc(nmasked);
-  // Per-workgroup address bases (q-head hk * G): a slot's loads add only the
-  // q-head and row offsets (a fifth fewer instructions per fast slot).
-  const char* q_head0 = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + static_cast<int64_t>(hk) * G * p.q.sh) * 2;
-  const char* do_head0 =
-      static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + static_cast<int64_t>(hk) * G * p.dout.sh) * 2;
-  const int64_t m_row0 = sv.mrow(b, hk * G, p.Hq, p.T, p.N);
-  const int64_t m_hstride = sv.packed ? p.T : p.N;  // M / Delta rows of consecutive q-heads
-  const i32x4_t q_rs = raw_rsrc(q_head0), do_rs = raw_rsrc(do_head0);
-  const int q_hs2 = static_cast<int>(p.q.sh * 2), q_ss2 = static_cast<int>(p.q.ss * 2);
-  const int do_hs2 = static_cast<int>(p.dout.sh * 2), do_ss2 = static_cast<int>(p.dout.ss * 2);
+  // Q / dO / M / Delta loads of a step (ssa_plan.hpp): per-workgroup address
+  // bases (q-head hk * G), so a slot's loads add only the q-head and row
+  // offsets (a fifth fewer instructions per fast slot).
+  const Loads ld(p, pl, wave, lane);
   auto issue = [&](int st, const StepWalk& w, auto unmasked_tag) {
-    if (st >= nsteps) return;
-    const int g = w.g;
-    const int q0 = qstart + (decltype(unmasked_tag)::value ? w.sub_unmasked(nlo) : w.sub(nlo, nsub)) * BMQ;
-    const uint32_t buf = bufof(st);
-    const char* qg = q_head0 + g * p.q.sh * 2;
-    const char* dog = do_head0 + g * p.dout.sh * 2;
-    if (q0 + BMQ <= N) {
-      if constexpr (OFF32) {
-        tile_load_pieces_off<D, BMQ, 4>(q_rs, g * q_hs2 + q0 * q_ss2, q_ss2, buf, wave, llq);
-        tile_load_pieces_off<D, BMQ, 4>(do_rs, g * do_hs2 + q0 * do_ss2, do_ss2, buf + TILE, wave, lld);
-      } else {
-        tile_load_pieces<D, BMQ, 4, false>(qg, p.q.ss, q0, N, buf, wave, llq);
-        tile_load_pieces<D, BMQ, 4, false>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
-      }
-    } else {
-      tile_load_pieces<D, BMQ, 4, true>(qg, p.q.ss, q0, N, buf, wave, llq);
-      tile_load_pieces<D, BMQ, 4, true>(dog, p.dout.ss, q0, N, buf + TILE, wave, lld);
-    }
-    if (wave == 3) {
-      const int64_t rw = m_row0 + g * m_hstride;
-      pair32_load_async(p.m + rw, p.delta + rw, q0, N, buf + 2 * TILE, lane);
-    }
+    ld.template issue<decltype(unmasked_tag)::value>(pl, st, w, lds0);
   };
   issue(0, wi, std::false_type{});
   wi.next(per_m, per_u, G);
@@ -408,30 +324,12 @@ __global__ __launch_bounds__(256, 1) void ssa_bwd_dkdv_kernel(BwdParams p) {
   // adjacent, so the lane writes two 16-byte pieces.
   // workspace tile (32 x 16) of q-head hk * G + g, query tile qi, key tile k0w / 16:
   // head_tile(b, hk G) + g tiles_per_head + row_offset(qi) + k0w / 16, 512 elements each
-  const int64_t ds_tph = ds_tiles_per_head(N, CAUSAL);
-  T* const ds_head0 =
-      static_cast<T*>(p.ds) + (ds_head_tile(sv.packed, sv.tok0, b, hk * G, p.Hq, N, p.N, CAUSAL) + (k0w >> 4)) * 512;
-  const uint32_t ds_lane = (l32 >> 4) * 512 + (l32 & 15) * 8;
   // Exactly two vector-memory instructions (the fast slot's load wait
-  // counts them): piece (g, t) at byte 256 g + 8 t of the lane's slot, so
-  // from 256 hh: +0 (g = hh, t = 0 and 1), +512 (g = 2 + hh).
-  const i32x4_t ds_rs = raw_rsrc(ds_head0);
-  const uint32_t ds_voff = (ds_lane + (16 * hh) * 8) * 2;
-  const int ds_tph1k = static_cast<int>(ds_tph * 1024);
+  // counts them), addressed by DkdvDsStores (ssa_plan.hpp).
+  const DkdvDsStores<CAUSAL, OFF32> dss(p, pl, k0w, lane);
   auto ds_store = [&](const StepWalk& w, const v8 (&s2)[2], auto unmasked_tag) {
-    const int q0 = qstart + (decltype(unmasked_tag)::value ? w.sub_unmasked(nlo) : w.sub(nlo, nsub)) * BMQ;
-    const u32x4 s0 = __builtin_bit_cast(u32x4, s2[0]), s1 = __builtin_bit_cast(u32x4, s2[1]);
-    if constexpr (OFF32) {
-      const int qi = q0 >> 5;
-      const int soff = __builtin_amdgcn_readfirstlane(w.g * ds_tph1k +
-                                                      (CAUSAL ? qi * (qi + 1) : qi * 2 * ((N + 31) >> 5)) * 1024);
-      buffer_store_b128_nt<0>(ds_rs, ds_voff, soff, u32x4{s0[0], s0[1], s1[0], s1[1]});
-      buffer_store_b128_nt<512>(ds_rs, ds_voff, soff, u32x4{s0[2], s0[3], s1[2], s1[3]});
-    } else {
-      T* dst = ds_head0 + (w.g * ds_tph + ds_row_offset(q0 >> 5, N, CAUSAL)) * 512 + ds_lane + (16 * hh) * 8;
-      store_b128_nt<0>(dst, u32x4{s0[0], s0[1], s1[0], s1[1]});
-      store_b128_nt<512>(dst, u32x4{s0[2], s0[3], s1[2], s1[3]});
-    }
+    const int q0 = pl.template q0<decltype(unmasked_tag)::value>(w);
+    dss.store(w.g, q0, __builtin_bit_cast(u32x4, s2[0]), __builtin_bit_cast(u32x4, s2[1]));
   };
   auto slot_generic = [&](int j) {
     wait_vm<0>();  // sub-tile j + 1
@@ -706,24 +604,20 @@ template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
-  constexpr int BM = 128, BN = 64;
+  using Plan = DqPlan<D, CAUSAL>;
+  constexpr int BM = Plan::BM, BN = Plan::BN;
   constexpr int ND16 = D / 16, ND32 = D / 32;
-  constexpr int TILE_BYTES = BN * D * 2;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * TILE_BYTES];
+  constexpr int TILE_BYTES = Plan::TILE;
+  __shared__ __attribute__((aligned(1024))) char smem[Plan::LDS_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int nqb = (p.N + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  // Logical order (head, sequence, query block), as in the forward.
-  int hb, rank;
-  dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
-  const int qb = nqb - 1 - rank;
-  const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
-  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
-  const int N = sv.N;
-  if (qb * BM >= N) return;  // packed: past the end of a shorter document
+  // dispatch and K / V tile loads (ssa_plan.hpp)
+  const Plan pl(p, blockIdx.x, gridDim.x);
+  if (pl.empty()) return;  // packed: past the end of a shorter document
+  const int qb = pl.qb, b = pl.b, h = pl.h, N = pl.N;
+  const SeqView& sv = pl.sv;
   const uint32_t lds0 = lds_addr(smem);
   const RowBase<D> rb(l32, hh);
   const TrBase<D> tb(lane);
@@ -731,8 +625,6 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
 
   const T* qg = static_cast<const T*>(p.q.ptr) + sv.off(p.q, b) + h * p.q.sh;
   const T* dog = static_cast<const T*>(p.dout.ptr) + sv.off(p.dout, b) + h * p.dout.sh;
-  const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
-  const char* vg = static_cast<const char*>(p.v.ptr) + (sv.off(p.v, b) + hk * p.v.sh) * 2;
 
   // n and b read once here: a read after the main loop would queue behind its
   // memory traffic and hold the workgroup's end for the round trip
@@ -742,12 +634,10 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
 
-  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  const int ntiles = pl.ntiles;
   const int nfull = CAUSAL ? min(q0 / BN, N / BN) : N / BN;
 
-  tile_load_async<D, BN, 4>(kg, p.k.ss, 0, N, lds0, wave, llk);
-  tile_load_async<D, BN, 4>(vg, p.v.ss, 0, N, lds0 + TILE_BYTES, wave, llv);
+  pl.load_tile(0, lds0, wave, llk, llv);
 
   v8 qf[ND16], dof[ND16];
 #pragma unroll
@@ -767,19 +657,9 @@ __global__ __launch_bounds__(256, 2) void ssa_bwd_dq_kernel(BwdParams p) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const uint32_t kl = lds0 + (t & 1) * 2 * TILE_BYTES;
+    const uint32_t kl = Plan::buf(lds0, t);
     const uint32_t vl = kl + TILE_BYTES;
-    if (t + 1 < ntiles) {
-      const uint32_t nk = lds0 + ((t + 1) & 1) * 2 * TILE_BYTES;
-      const int r1 = (t + 1) * BN;
-      if (r1 + BN <= N) {
-        tile_load_pieces<D, BN, 4, false>(kg, p.k.ss, r1, N, nk, wave, llk);
-        tile_load_pieces<D, BN, 4, false>(vg, p.v.ss, r1, N, nk + TILE_BYTES, wave, llv);
-      } else {
-        tile_load_pieces<D, BN, 4, true>(kg, p.k.ss, r1, N, nk, wave, llk);
-        tile_load_pieces<D, BN, 4, true>(vg, p.v.ss, r1, N, nk + TILE_BYTES, wave, llv);
-      }
-    }
+    if (t + 1 < ntiles) pl.load_tile(t + 1, lds0, wave, llk, llv);
     const RowBase<D> rk = at_tile(rb, kl), rv = at_tile(rb, vl);
     const TrBase<D> tk = at_tile(tb, kl);
     const int kbase = t * BN;
@@ -900,16 +780,12 @@ template <typename T, int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
-  using BL = BlockLayout<D>;
-  constexpr int BM = 32 * NW, BN = 64, ND32 = D / 32;
-  constexpr int NK = 2, PFK = 1, NDS = 3, PFD = 2;
-  constexpr int KTILE = BN * D * 2;
-  constexpr int DSTAGE = NW * 4096;             // NW waves x 4 dS' tiles
-  constexpr int KP = (BN / 32) * BL::IPB / NW;  // K load pieces per wave and tile
-  static_assert(KP >= 1, "K tile split");
-  static_assert(PFD > PFK && PFK >= 1 && PFK < NK && PFD < NDS, "ring depths");
+  using Loads = DqDsLoads<D, CAUSAL, NW>;
+  constexpr int ND32 = D / 32;
+  constexpr int NK = Loads::NK, PFK = Loads::PFK, PFD = Loads::PFD;
+  constexpr int KTILE = Loads::KTILE, DSTAGE = Loads::DSTAGE, KP = Loads::KP;
   static_assert(NW * 64 >= 256, "the fused reduction needs 256 threads");
-  __shared__ __attribute__((aligned(1024))) char smem[NK * KTILE + NDS * DSTAGE];
+  __shared__ __attribute__((aligned(1024))) char smem[Loads::LDS_BYTES];
   __shared__ float red_sh[2][256];
 
   // The backward's dn / db reduction, before this workgroup issues any load
@@ -921,15 +797,11 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nqb = (p.N + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  int hb, rank;
-  dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
-  const int qb = CAUSAL ? nqb - 1 - rank : rank;
-  const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
-  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
-  const int N = sv.N;
-  if (qb * BM >= N) return;  // packed: past the end of a shorter document
+  // dispatch, K tile and dS' tile loads (ssa_plan.hpp)
+  const Loads ld(p, blockIdx.x, gridDim.x, wave, lane);
+  if (ld.empty()) return;  // packed: past the end of a shorter document
+  const int b = ld.b, h = ld.h, N = ld.N;
+  const SeqView& sv = ld.sv;
   // the workspace holds -dS' (the dK/dV kernel's sign convention); n and b
   // are read before the stream starts (read after it, the two loads queue
   // behind the workspace traffic and hold the workgroup's end: 25 % of the
@@ -938,32 +810,20 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t lds_ds = lds0 + NK * KTILE;
   // K tiles: row-swizzled for D = 128 (whole-row loads), block-chunk-major otherwise
-  constexpr bool ROWSWZ = D == 128;
+  constexpr bool ROWSWZ = Loads::ROWSWZ;
   const TrBase<D> tb(lane);
-  const LoadLane llk(lane, wave, p.k.ss);
   const RowSwzTr rtb(lane);
-  const RowSwzLoad rlk(lane, p.k.ss);
 
-  const int q0 = qb * BM;
-  const int wq0 = q0 + wave * 32;
-  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  const int wq0 = ld.wq0;
+  const int ntiles = ld.ntiles;
   // dS' tiles of this wave's query rows: kj < nkj (loads clamped to kj_max)
-  const int nk16 = (N + 15) / 16;
-  const int nkj = wq0 >= N ? 0 : (CAUSAL ? min(2 * (wq0 >> 5) + 2, nk16) : nk16);
-  const int kj_max = nkj > 0 ? nkj - 1 : 0;
-  // the wave's row of workspace tiles (at most 2 nq32 KB: 32-bit offsets)
-  const i32x4_t ds_rsrc =
-      raw_rsrc(static_cast<const char*>(p.ds) + (ds_head_tile(sv.packed, sv.tok0, b, h, p.Hq, N, p.N, CAUSAL) +
-                                                 ds_row_offset(min(wq0, N - 1) >> 5, N, CAUSAL)) * 1024);
-  const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
+  const int nkj = ld.nkj;
   // A stored tile holds, in lane s = 16 g + kl, key kl and queries 16 t + 4 g +
   // (0..3) (elements 4 t ..).  LDS slot 16 g + m receives stored lane
-  // 16 g + (m ^ 4 g); the B operand (query L % 32, keys 8 r + 4 hh + e) is then
-  // two transposed reads, lane i of group G supplying key 8 r + 4 hh + i / 4,
-  // queries 16 (G & 1) + 4 (i % 4) .. + 3, and each half-wave covers every
-  // bank once.
-  const uint32_t ds_src = static_cast<uint32_t>((16 * (lane >> 4) + ((lane & 15) ^ (4 * (lane >> 4)))) * 16);
+  // 16 g + (m ^ 4 g) (the loads' lane order); the B operand (query L % 32,
+  // keys 8 r + 4 hh + e) is then two transposed reads, lane i of group G
+  // supplying key 8 r + 4 hh + i / 4, queries 16 (G & 1) + 4 (i % 4) .. + 3,
+  // and each half-wave covers every bank once.
   uint32_t ds_rd[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -972,18 +832,8 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
     ds_rd[r] = static_cast<uint32_t>((16 * gp + (key ^ (4 * gp))) * 16 + 8 * (G & 1));
   }
 
-  auto issue_k = [&](int t) {
-    if constexpr (ROWSWZ)
-      rowswz_load<BN, NW>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, rlk);
-    else
-      tile_load_async<D, BN, NW>(kg, p.k.ss, t * BN, N, lds0 + (t % NK) * KTILE, wave, llk);
-  };
-  auto issue_ds = [&](int t) {
-    const uint32_t dst = lds_ds + (t % NDS) * DSTAGE + wave * 4096;
-#pragma unroll
-    // dS' is read exactly once: streaming cache policy
-    for (int s4 = 0; s4 < 4; ++s4) dma_buffer16<true>(dst + s4 * 1024, ds_rsrc, ds_src, min(4 * t + s4, kj_max) * 1024);
-  };
+  auto issue_k = [&](int t) { ld.issue_k(t, lds0); };
+  auto issue_ds = [&](int t) { ld.issue_ds(t, lds0); };
 
   f32x16 dq[ND32];
 #pragma unroll
@@ -1000,9 +850,9 @@ __global__ __launch_bounds__(NW * 64) void ssa_bwd_dq_ds_kernel(BwdParams p) {
     __builtin_amdgcn_s_barrier();
     issue_k(t + PFK);
     issue_ds(t + PFD);
-    const TrBase<D> tk = at_tile(tb, lds0 + (t % NK) * KTILE);
-    const RowSwzTr rk = at_tile(rtb, lds0 + (t % NK) * KTILE);
-    const uint32_t dsl = lds_ds + (t % NDS) * DSTAGE + wave * 4096;
+    const TrBase<D> tk = at_tile(tb, Loads::ktile(lds0, t));
+    const RowSwzTr rk = at_tile(rtb, Loads::ktile(lds0, t));
+    const uint32_t dsl = ld.dstage(lds0, t);
     typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
@@ -1063,16 +913,6 @@ hipError_t launch_bwd_preprocess(const BwdParams& p, int dtype, int D, hipStream
   return dtype == 0 ? pre_dt<__bf16>(p, D, s) : pre_dt<_Float16>(p, D, s);
 }
 
-// Whether every dK/dV workgroup's Q / dO rows (from q-head hk G of its
-// sequence: G heads, N rows, D columns) and its dS' tiles (G triangles of
-// the longest sequence) lie below 2 GiB of their bases; strides are
-// non-negative (validated at the boundary).
-static bool dkdv_off32(const BwdParams& p, int D, bool causal) {
-  const int64_t G = p.Hq / p.Hkv, lim = (int64_t{1} << 31) - 4096;
-  auto span = [&](const Tensor4& t) { return ((G - 1) * t.sh + static_cast<int64_t>(p.N - 1) * t.ss + D) * 2; };
-  if (span(p.q) >= lim || span(p.dout) >= lim) return false;
-  return p.ds == nullptr || G * ds_tiles_per_head(p.N, causal) * 1024 < lim;
-}
 
 // SSA_DKDV2W=1 selects the two-waves-per-SIMD dK/dV kernel
 // (ssa_bwd_dkdv2w.hip) for bf16 / fp16; read at every launch, so a caller
@@ -1084,7 +924,7 @@ static bool use_dkdv2w() {
 
 template <typename T, int D, bool CAUSAL>
 static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
-  const int grid = dkdv_key_blocks(p.N) * p.B * p.Hkv;
+  const int grid = DkdvPlan<128, 32, CAUSAL>::grid(p);
   const bool o32 = dkdv_off32(p, D, CAUSAL);
   if (use_dkdv2w()) return launch_bwd_dkdv2w(p, std::is_same_v<T, __bf16> ? 0 : 1, D, CAUSAL, o32, s);
   if (p.ds != nullptr) {
@@ -1101,23 +941,14 @@ static hipError_t dkdv_t(const BwdParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// dS' K pass: 8 waves (256 queries per workgroup; 128 KB of LDS at head dim
-// 128, 112 KB at 64) at head dims 64 and 128, so each K tile is read once per
-// 256 queries (measured 4 % faster than 4-wave workgroups at both); 4 waves
-// at head dim 32.
-template <int D>
-constexpr int dq_ds_waves() {
-  return D >= 64 ? 8 : 4;
-}
-
 template <typename T, int D, bool CAUSAL>
 static hipError_t dq_t(const BwdParams& p, hipStream_t s) {
   if (p.ds != nullptr) {
     constexpr int NW = dq_ds_waves<D>();
-    const int grid = ((p.N + 32 * NW - 1) / (32 * NW)) * p.B * p.Hq;
+    const int grid = DqDsLoads<D, CAUSAL, NW>::grid(p);
     hipLaunchKernelGGL((ssa_bwd_dq_ds_kernel<T, D, CAUSAL, NW>), dim3(grid), dim3(NW * 64), 0, s, p);
   } else {
-    const int grid = ((p.N + 127) / 128) * p.B * p.Hq;
+    const int grid = DqPlan<D, CAUSAL>::grid(p);
     hipLaunchKernelGGL((ssa_bwd_dq_kernel<T, D, CAUSAL>), dim3(grid), dim3(256), 0, s, p);
   }
   return hipGetLastError();

@@ -38,6 +38,7 @@
 
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
+#include "ssa_plan.hpp"
 #include "ssa_tile.hpp"
 
 namespace ssa {
@@ -112,32 +113,6 @@ __device__ __forceinline__ void wait_vm_dyn(int n) {
   }
 }
 
-// 64 consecutive fp32 (rows row0.., clamped to nrows - 1) into 256 bytes of LDS.
-__device__ __forceinline__ void vec64_load_async(const float* a, int row0, int nrows, uint32_t lds, int lane) {
-  int r = row0 + lane;
-  r = r < nrows ? r : nrows - 1;
-  dma_global4(lds, a + r);
-}
-
-// Step st of a workgroup -> (q-head g, 64-query sub-tile i), masked sub-tiles
-// of every q-head first (the nlo diagonal ones, then a partial last one),
-// then the unmasked ones; walked without divisions (as ssa_bwd.hip).
-struct StepWalk2 {
-  int g, j;
-  bool unmasked;
-  __device__ __forceinline__ explicit StepWalk2(int nmasked) : g(0), j(0), unmasked(nmasked == 0) {}
-  __device__ __forceinline__ void next(int per_m, int per_u, int G) {
-    ++j;
-    if (j >= (unmasked ? per_u : per_m)) {
-      j = 0;
-      if (++g >= G) {
-        g = 0;
-        unmasked = true;
-      }
-    }
-  }
-  __device__ __forceinline__ int sub(int nlo, int nsub) const { return unmasked ? nlo + j : (j < nlo ? j : nsub - 1); }
-};
 
 // MFMA schedule of a slot: item index -> kind and tick.  Items in order:
 //   H1: dV/dK of step j - 1, query half 1 (2 NDB: dV, dK per column block)
@@ -205,29 +180,25 @@ template <typename T, int D, bool CAUSAL, bool DS, bool OFF32>
 __global__ __launch_bounds__(512, 1) void ssa_bwd_dkdv2w_kernel(BwdParams p) {
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
-  constexpr int NW = 8, KW = 16, BN = NW * KW, BMQ = 64, NB = 4;
-  static_assert(BN == 128, "dkdv_key_blocks() counts 128-key blocks");
+  using Loads = Dkdv2wLoads<D, CAUSAL, OFF32, kSpread>;
+  using Plan = typename Loads::Plan;
+  constexpr int NW = Loads::NW, KW = Loads::KW, NB = Loads::NB;
   using SC = Sched2w<D>;
   using TL = Swz8Tile<D>;
   constexpr int NKS = SC::NKS, NDB = SC::NDB;
   constexpr int TILE = TL::TILE;
-  constexpr int BUF = 2 * TILE + 512;  // Q, dO, M[64], Delta[64]
-  constexpr int NPIECE = TILE / 1024;  // 1 KB loads per tile
-  __shared__ __attribute__((aligned(1024))) char smem[NB * BUF];
+  static_assert(TILE == Loads::TILE, "tile size");
+  __shared__ __attribute__((aligned(1024))) char smem[Loads::LDS_BYTES];
   __shared__ float red[2][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, i16 = lane & 15;
-  const int nkb = dkdv_key_blocks(p.N);
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  int bhk, kb;
-  dispatch_order(L, gridDim.x / nkb, nkb, p.cu_seqlens ? 1 : kOrderGroup, bhk, kb);
-  const int b = bhk % p.B, hk = bhk / p.B;
-  const int G = p.Hq / p.Hkv;
-  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
-  const int N = sv.N;
-  if (kb * BN >= N) {  // packed: past the end of a shorter document
+  // dispatch and step order (ssa_plan.hpp)
+  const Plan pl(p, blockIdx.x, gridDim.x);
+  const int nkb = pl.nkb, bhk = pl.bhk, kb = pl.kb, b = pl.b, hk = pl.hk, G = pl.G, N = pl.N;
+  const SeqView& sv = pl.sv;
+  if (pl.empty()) {  // packed: past the end of a shorter document
     if (tid == 0) {
       const int64_t P = static_cast<int64_t>(p.B) * p.Hkv * nkb;
       p.partials[static_cast<int64_t>(bhk) * nkb + kb] = 0.f;
@@ -238,109 +209,35 @@ __global__ __launch_bounds__(512, 1) void ssa_bwd_dkdv2w_kernel(BwdParams p) {
   const float n = *p.n_ptr, bv = *p.b_ptr;
   const float c = p.scale * bv;
   const uint32_t lds0 = lds_addr(smem);
-  const LoadLane llq(lane, p.q.ss, LoadLane::Swz8{}), lld(lane, p.dout.ss, LoadLane::Swz8{});
 
-  const int k0 = kb * BN;
+  const int k0 = pl.k0;
   const int k0w = k0 + wave * KW;
   const int key = k0w + i16;
   const T* kg = static_cast<const T*>(p.k.ptr) + sv.off(p.k, b) + hk * p.k.sh;
   const T* vg = static_cast<const T*>(p.v.ptr) + sv.off(p.v, b) + hk * p.v.sh;
 
-  const int qstart = CAUSAL ? k0 : 0;
-  const int nsub = (N - qstart + BMQ - 1) / BMQ;
-  const int nsteps = G * nsub;
-  const bool key_edge = k0 + BN > N;
-  const int nlo = key_edge ? nsub : (CAUSAL ? min(BN / BMQ, nsub) : 0);
-  const int ntail = (!key_edge && (N % BMQ) != 0 && nsub > nlo) ? 1 : 0;
-  const int per_m = nlo + ntail, per_u = nsub - per_m;
-  const int nmasked = G * per_m;
-  auto bufof = [&](int st) { return lds0 + (st & (NB - 1)) * BUF; };
+  const int nsteps = pl.nsteps;
+  const int per_m = pl.per_m, per_u = pl.per_u, nmasked = pl.nmasked;
+  auto bufof = [&](int st) { return Loads::buf(lds0, st); };
 
-  StepWalk2 wi(nmasked), wc(nmasked);
-  const char* q_head0 = static_cast<const char*>(p.q.ptr) + (sv.off(p.q, b) + static_cast<int64_t>(hk) * G * p.q.sh) * 2;
-  const char* do_head0 =
-      static_cast<const char*>(p.dout.ptr) + (sv.off(p.dout, b) + static_cast<int64_t>(hk) * G * p.dout.sh) * 2;
-  const int64_t m_row0 = sv.mrow(b, hk * G, p.Hq, p.T, p.N);
-  const int64_t m_hstride = sv.packed ? p.T : p.N;
-  const i32x4_t q_rs = raw_rsrc(q_head0), do_rs = raw_rsrc(do_head0);
-  const int q_hs2 = static_cast<int>(p.q.sh * 2), q_ss2 = static_cast<int>(p.q.ss * 2);
-  const int do_hs2 = static_cast<int>(p.dout.sh * 2), do_ss2 = static_cast<int>(p.dout.ss * 2);
-  // dO pieces from the upper waves when a tile has fewer pieces than waves
-  const int wave_do = NPIECE < NW ? (wave + NW / 2) % NW : wave;
-  // A tile whose loads issue() deferred to issue_piece() (kSpread).
-  struct Deferred {
-    bool on;
-    uint32_t buf;
-    int qoff, doff, q0;
-    int64_t rw;
-  } dfr{false, 0, 0, 0, 0, 0};
-  auto issue = [&](int st, const StepWalk2& w) {
-    dfr.on = false;
-    if (st >= nsteps) return;
-    const int g = w.g;
-    const int q0 = qstart + w.sub(nlo, nsub) * BMQ;
-    const uint32_t buf = bufof(st);
-    const char* qg = q_head0 + g * p.q.sh * 2;
-    const char* dog = do_head0 + g * p.dout.sh * 2;
-    const int64_t rw = m_row0 + g * m_hstride;
-    if (q0 + BMQ <= N) {
-      if constexpr (OFF32 && kSpread) {
-        dfr = Deferred{true, buf, __builtin_amdgcn_readfirstlane(g * q_hs2 + q0 * q_ss2),
-                       __builtin_amdgcn_readfirstlane(g * do_hs2 + q0 * do_ss2), q0, rw};
-        return;
-      } else if constexpr (OFF32) {
-        tile_load_pieces_off<D, BMQ, NW>(q_rs, g * q_hs2 + q0 * q_ss2, q_ss2, buf, wave, llq);
-        tile_load_pieces_off<D, BMQ, NW>(do_rs, g * do_hs2 + q0 * do_ss2, do_ss2, buf + TILE, wave_do, lld);
-      } else {
-        tile_load_pieces<D, BMQ, NW, false>(qg, p.q.ss, q0, N, buf, wave, llq);
-        tile_load_pieces<D, BMQ, NW, false>(dog, p.dout.ss, q0, N, buf + TILE, wave_do, lld);
-      }
-    } else {
-      tile_load_pieces<D, BMQ, NW, true>(qg, p.q.ss, q0, N, buf, wave, llq);
-      tile_load_pieces<D, BMQ, NW, true>(dog, p.dout.ss, q0, N, buf + TILE, wave_do, lld);
-    }
-    // M and Delta: each wave loads the 8 rows of its own eighth of the lanes,
-    // so that every wave issues LPT loads per tile (exact vmcnt counts)
-    if ((lane >> 3) == wave) {
-      vec64_load_async(p.m + rw, q0, N, buf + 2 * TILE, lane);
-      vec64_load_async(p.delta + rw, q0, N, buf + 2 * TILE + 256, lane);
-    }
-  };
+  StepWalk wi(nmasked), wc(nmasked);
+  // Q / dO / M / Delta loads of a step (ssa_plan.hpp); in the steady state
+  // (kSpread) issue() only prepares a tile and issue_piece<K>() issues its
+  // loads one at a time.
+  Loads ld(p, pl, wave, lane);
+  auto issue = [&](int st, const StepWalk& w) { ld.issue(pl, st, w, lds0); };
   // vector-memory operations per wave and tile that the waits below count:
   // Q and dO pieces (D = 32: one of the two), M, Delta
-  constexpr int LPT = (NPIECE >= NW ? 2 * NPIECE / NW : 1) + 2;
-  // Load K of a deferred tile, K = 0 .. NLD - 1 over the Q / dO pieces
-  // (alternating), then M and Delta; every wave issues LPT of them.
-  constexpr int PQ = NPIECE >= NW ? NPIECE / NW : 1;
-  constexpr int NLD = 2 * PQ + 2;
-  auto issue_piece = [&](auto kc) {
-    constexpr int K = decltype(kc)::value;
-    if (!dfr.on) return;
-    if constexpr (K < 2 * PQ) {
-      constexpr bool DO = K % 2 == 1;
-      const int j = (DO ? wave_do : wave) + NW * (K / 2);
-      if (NPIECE % NW != 0 && j >= NPIECE) return;
-      constexpr int IPB = BlockLayout<D>::IPB;
-      const int blk = j / IPB, cp = j % IPB;
-      if constexpr (DO)
-        dma_buffer16(dfr.buf + TILE + j * 1024, do_rs, lld.off, dfr.doff + blk * 32 * do_ss2 + cp * 32);
-      else
-        dma_buffer16(dfr.buf + j * 1024, q_rs, llq.off, dfr.qoff + blk * 32 * q_ss2 + cp * 32);
-    } else if ((lane >> 3) == wave) {
-      if constexpr (K == 2 * PQ)
-        vec64_load_async(p.m + dfr.rw, dfr.q0, N, dfr.buf + 2 * TILE, lane);
-      else
-        vec64_load_async(p.delta + dfr.rw, dfr.q0, N, dfr.buf + 2 * TILE + 256, lane);
-    }
-  };
+  constexpr int LPT = Loads::LPT;
+  constexpr int NLD = Loads::NLD;
+  auto issue_piece = [&](auto kc) { ld.template issue_piece<decltype(kc)::value>(N); };
   // deferred loads of the prologue's tiles are issued at once
-  auto issue_all = [&](int st, const StepWalk2& w) {
+  auto issue_all = [&](int st, const StepWalk& w) {
     issue(st, w);
     [&]<int... k>(std::integer_sequence<int, k...>) {
       (issue_piece(std::integral_constant<int, k>{}), ...);
     }(std::make_integer_sequence<int, NLD>{});
   };
-  static_assert(NPIECE >= NW || 2 * NPIECE == NW, "every wave loads the same number of pieces");
   auto loads_of = [&](int st) { return st < nsteps ? LPT : 0; };
   // tiles 0 .. 2 (kDeep) or 0 .. 1 in flight
   constexpr int AHEAD = kDeep ? 3 : 2;
@@ -397,43 +294,14 @@ __global__ __launch_bounds__(512, 1) void ssa_bwd_dkdv2w_kernel(BwdParams p) {
   // dS' workspace: this wave's key tile k0w / 16 of query tiles qt (the
   // stored layout is the lane layout of sa[h]: lane 16 g + i holds key i,
   // queries 16 t + 4 g + (0..3) in elements 4 t ..).
-  const int64_t ds_tph = ds_tiles_per_head(N, CAUSAL);
-  char* const ds_head0 = static_cast<char*>(p.ds) +
-                         (ds_head_tile(sv.packed, sv.tok0, b, hk * G, p.Hq, N, p.N, CAUSAL) + (k0w >> 4)) * 1024;
-  const i32x4_t ds_rs = raw_rsrc(ds_head0);
-  const uint32_t ds_voff = static_cast<uint32_t>(lane * 16);
-  const int ds_tph1k = static_cast<int>(ds_tph * 1024);
-  const int nq32 = (N + 31) >> 5;
+  const Dkdv2wDsStores<CAUSAL, OFF32> dss(p, pl, k0w, lane);
   // Stores of step (g, q0), tiles hq = 0, 1 with mask bits `which`.
   auto ds_store = [&](int g, int q0, int which) {
 #pragma unroll
-    for (int hq = 0; hq < 2; ++hq) {
-      if (!(which & (1 << hq))) continue;
-      const int qt = (q0 >> 5) + hq;
-      const u32x4 v = __builtin_bit_cast(u32x4, sa[hq]);
-      if constexpr (OFF32) {
-        const int soff = __builtin_amdgcn_readfirstlane(
-            g * ds_tph1k + (CAUSAL ? qt * (qt + 1) : qt * 2 * nq32) * 1024);
-        buffer_store_b128_nt<0>(ds_rs, ds_voff, soff, v);
-      } else {
-        char* dst = ds_head0 + (g * ds_tph + ds_row_offset(qt, N, CAUSAL)) * 1024 + ds_voff;
-        store_b128_nt<0>(dst, v);
-      }
-    }
+    for (int hq = 0; hq < 2; ++hq)
+      if (which & (1 << hq)) dss.store(g, q0, hq, __builtin_bit_cast(u32x4, sa[hq]));
   };
-  // Which of the two 32-query tiles of a masked step this wave stores: tiles
-  // inside the sequence whose queries reach this wave's keys (exactly the
-  // tiles of the causal triangle the dQ pass reads).
-  auto ds_which = [&](int q0) {
-    if (k0w >= N) return 0;
-    int w = 0;
-#pragma unroll
-    for (int hq = 0; hq < 2; ++hq) {
-      const int qt0 = q0 + 32 * hq;
-      if (qt0 < N && (!CAUSAL || qt0 + 31 >= k0w)) w |= 1 << hq;
-    }
-    return w;
-  };
+  auto ds_which = [&](int q0) { return dss.which(q0); };
 
   // ---- one slot: element pipeline of step j, MFMAs of steps j - 1, j, j + 1 ----
   // The workgroup synchronises once per slot, at tick SYNC: every wave is then
@@ -451,7 +319,7 @@ __global__ __launch_bounds__(512, 1) void ssa_bwd_dkdv2w_kernel(BwdParams p) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool SWAP = decltype(swap_tag)::value;
     const int gq = wc.g;
-    const int q0 = qstart + wc.sub(nlo, nsub) * BMQ;
+    const int q0 = pl.template q0<false>(wc);
     const int qm = q0 + 4 * g4;  // query of element e: qm + 16 (e >> 2) + (e & 3)
     const uint32_t bprev = bufof(j - 1), bcur = bufof(j), bnext = bufof(j + 1);
     const uint32_t tr_prev = opaque(bprev + trb), tr_cur = opaque(bcur + trb);
@@ -717,7 +585,7 @@ __global__ __launch_bounds__(512, 1) void ssa_bwd_dkdv2w_kernel(BwdParams p) {
 
 template <typename T, int D, bool CAUSAL>
 static hipError_t dkdv2w_t(const BwdParams& p, bool off32, hipStream_t s) {
-  const int grid = dkdv_key_blocks(p.N) * p.B * p.Hkv;
+  const int grid = DkdvPlan<128, 64, CAUSAL>::grid(p);
   if (p.ds != nullptr) {
     if (off32)
       hipLaunchKernelGGL((ssa_bwd_dkdv2w_kernel<T, D, CAUSAL, true, true>), dim3(grid), dim3(512), 0, s, p);

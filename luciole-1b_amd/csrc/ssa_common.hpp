@@ -109,7 +109,7 @@ __device__ __forceinline__ float pair_sum(float x) {
 // Workgroups are dispatched round-robin over the 8 XCDs (block id % 8).  This
 // bijection on [0, total) gives each XCD a contiguous range of logical block
 // indices, so logical neighbours (same head) share one XCD's L2.
-__device__ __forceinline__ int xcd_remap(int bid, int total) {
+__host__ __device__ __forceinline__ int xcd_remap(int bid, int total) {
   const int q = total >> 3, r = total & 7;
   const int x = bid & 7, j = bid >> 3;
   return x * q + (x < r ? x : r) + j;
@@ -128,9 +128,9 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // of a pair are documents of different lengths, whose block weights the rank
 // does not describe (measured: pairs cost the packed benchmark 15 %).
 constexpr int kOrderGroup = 2;
-__device__ __forceinline__ void dispatch_order(int L, int nhb, int nblk, int group, int& hb, int& rank) {
+__host__ __device__ __forceinline__ void dispatch_order(int L, int nhb, int nblk, int group, int& hb, int& rank) {
   const int g = L / (group * nblk), r = L - g * group * nblk;
-  const int gs = min(group, nhb - g * group);  // >= 1 for L < nhb * nblk
+  const int gs = group < nhb - g * group ? group : nhb - g * group;  // >= 1 for L < nhb * nblk
   hb = g * group + r % gs;
   rank = r / gs;
 }
@@ -194,6 +194,18 @@ struct DecodeParams {
   float scale;
 };
 
+// An entry of a table every lane of the workgroup reads at the same index
+// (the packed batches' document table), read through the global address
+// space: a scalar load with a wave-uniform result even where the compiler
+// cannot trace the pointer back to a kernel argument.
+__host__ __device__ __forceinline__ int load_table_entry(const int* t, int i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return ((const __attribute__((address_space(1))) int*)t)[i];
+#else
+  return t[i];
+#endif
+}
+
 // The sequence a workgroup works on.  For packed batches the document table
 // is clamped to [0, T] and the length to N, so any table keeps every access
 // inside the token stream.
@@ -201,10 +213,11 @@ struct SeqView {
   int N;         // length of this sequence
   int64_t tok0;  // packed: first token of the document
   bool packed;
-  __device__ __forceinline__ SeqView(const int* cu, int T, int Nmax, int b) {
+  __host__ __device__ __forceinline__ SeqView() : N(0), tok0(0), packed(false) {}
+  __host__ __device__ __forceinline__ SeqView(const int* cu, int T, int Nmax, int b) {
     packed = cu != nullptr;
     if (packed) {
-      int s0 = cu[b], s1 = cu[b + 1];
+      int s0 = load_table_entry(cu, b), s1 = load_table_entry(cu, b + 1);
       s0 = s0 < 0 ? 0 : (s0 > T ? T : s0);
       s1 = s1 < s0 ? s0 : (s1 > T ? T : s1);
       tok0 = s0;
@@ -215,9 +228,9 @@ struct SeqView {
     }
   }
   // element offset of the sequence in a tensor (before the head offset)
-  __device__ __forceinline__ int64_t off(const Tensor4& t, int b) const { return packed ? tok0 * t.ss : b * t.sb; }
+  __host__ __device__ __forceinline__ int64_t off(const Tensor4& t, int b) const { return packed ? tok0 * t.ss : b * t.sb; }
   // index of row 0 of (b, h) in M / Delta
-  __device__ __forceinline__ int64_t mrow(int b, int h, int H, int T, int Nmax) const {
+  __host__ __device__ __forceinline__ int64_t mrow(int b, int h, int H, int T, int Nmax) const {
     return packed ? static_cast<int64_t>(h) * T + tok0 : (static_cast<int64_t>(b) * H + h) * Nmax;
   }
 };

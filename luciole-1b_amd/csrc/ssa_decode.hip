@@ -27,44 +27,17 @@
 // combines in split order (deterministic).
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
+#include "ssa_plan.hpp"
 #include "ssa_tile.hpp"
 
 namespace ssa {
 
 namespace {
 
-template <int D>
-struct DecodeCfg {
-  static constexpr int NW = D == 128 ? 4 : 8;                      // waves per workgroup
-  static constexpr int BLOCK = BlockLayout<D>::BLOCK;             // one 32-row K or V block
-  static constexpr int TB = 2 * BLOCK;                            // K block, then V block
-  static constexpr int NB = 131072 / (NW * TB);                   // ring depth per wave
-  static constexpr int LPT = 2 * BlockLayout<D>::IPB;             // loads per tile
-  static constexpr int SMEM = NW * NB * TB;                       // 128 KB
-  static constexpr int ACC_LD = D + 1;                            // merge row stride (floats)
-  static constexpr int ML_BYTES = NW * 2 * 32 * 4;                // merge (m, l) per wave and q-head
-  static_assert(NB >= 2 && (NB - 1) * LPT < 64, "ring depth");
-  static_assert(ML_BYTES + NW * 32 * ACC_LD * 4 <= SMEM, "merge area");
-};
-
-// Rows row0 .. row0 + 31 (clamped to nrows - 1) of a [*, D] matrix with row
-// stride `ss` elements into one LDS block at `dst`, in the tile layout of
-// ssa_tile.hpp, issued by a single wave: piece j (1 KB) holds chunks 2 j and
-// 2 j + 1, whose swizzle parity is j & 1, hence the two LoadLane variants.
-template <int D>
-__device__ __forceinline__ void block_load_wave(const char* g, int64_t ss, int row0, int nrows, uint32_t dst,
-                                                const LoadLane& ll0, const LoadLane& ll1) {
-#pragma unroll
-  for (int j = 0; j < BlockLayout<D>::IPB; ++j) {
-    const LoadLane& ll = (j & 1) ? ll1 : ll0;
-    int row = row0 + ll.r;
-    row = row < nrows ? row : nrows - 1;
-    dma_global16(dst + j * 1024, g + (static_cast<int64_t>(row) * ss + j * 16) * 2 + ll.hoff);
-  }
-}
+// DecodeCfg, DecodePlan and block_load_wave: ssa_plan.hpp.
 
 template <typename T, int D, bool NPOS>
-__device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, int b, int hk, int qg, int split) {
+__device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, const DecodePlan<D>& pl) {
   typedef DecodeCfg<D> C;
   typedef typename Vec8<T>::type v8;
   typedef T v4 __attribute__((ext_vector_type(4)));
@@ -73,16 +46,13 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, i
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
+  const int b = pl.b, hk = pl.hk, qg = pl.qg, split = pl.split;
   const int G = p.Hq / p.Hkv;
   const int gq = min(32, G - qg * 32);  // q-heads of this group
   const int h0 = hk * G + qg * 32;      // first q-head of the group
 
-  int L = p.seqlens[b];
-  L = L < 0 ? 0 : (L > p.cap ? p.cap : L);
-  const int kbeg = split * p.split_keys;
-  const int kend = min(L, kbeg + p.split_keys);
-  const int ntile = kend > kbeg ? (kend - kbeg + 31) / 32 : 0;
-  const int ntw = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;  // tiles of this wave
+  const int kbeg = pl.kbeg, kend = pl.kend;
+  const int ntw = pl.tiles_of(wave);  // tiles of this wave
 
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;  // u = c * |q.k|
@@ -100,8 +70,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, i
   float m_run = -INFINITY, l_run = 0.f;
 
   if (ntw > 0) {
-    const char* kg = static_cast<const char*>(p.k.ptr) + (b * p.k.sb + hk * p.k.sh) * 2;
-    const char* vg = static_cast<const char*>(p.v.ptr) + (b * p.v.sb + hk * p.v.sh) * 2;
     const LoadLane lk0(lane, 0, p.k.ss), lk1(lane, 1, p.k.ss), lv0(lane, 0, p.v.ss), lv1(lane, 1, p.v.ss);
     const uint32_t ring = lds_addr(smem) + wave * NB * C::TB;
     const RowBase<D> rb(l32, hh);
@@ -109,12 +77,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, i
     // The i-th tile of this wave; past the wave's last tile the rows clamp to
     // kend - 1 (loads into a free buffer, never read), so every iteration
     // issues the same number of loads and one wait count fits all.
-    auto issue = [&](int i) {
-      const int row0 = kbeg + 32 * (wave + NW * i);
-      const uint32_t dst = ring + (i % NB) * C::TB;
-      block_load_wave<D>(kg, p.k.ss, row0, kend, dst, lk0, lk1);
-      block_load_wave<D>(vg, p.v.ss, row0, kend, dst + C::BLOCK, lv0, lv1);
-    };
+    auto issue = [&](int i) { pl.issue(i, wave, ring, lk0, lk1, lv0, lv1); };
 #pragma unroll
     for (int i = 0; i < NB - 1; ++i) issue(i);
     for (int i = 0; i < ntw; ++i) {
@@ -220,17 +183,11 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p, char* smem, i
 template <typename T, int D>
 __global__ __launch_bounds__(DecodeCfg<D>::NW * 64) void ssa_decode_kernel(DecodeParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[DecodeCfg<D>::SMEM];
-  const int nqg = (p.Hq / p.Hkv + 31) / 32;
-  int u = blockIdx.x;
-  const int split = u % p.splits;
-  u /= p.splits;
-  const int qg = u % nqg;
-  u /= nqg;
-  const int hk = u % p.Hkv, b = u / p.Hkv;
+  const DecodePlan<D> pl(p, blockIdx.x);
   if (*p.n_ptr >= 0.f)
-    decode_body<T, D, true>(p, smem, b, hk, qg, split);
+    decode_body<T, D, true>(p, smem, pl);
   else
-    decode_body<T, D, false>(p, smem, b, hk, qg, split);
+    decode_body<T, D, false>(p, smem, pl);
 }
 
 // One thread per output element d of a (sequence, q-head): combine the split
@@ -269,8 +226,7 @@ __global__ __launch_bounds__(128) void ssa_decode_merge_kernel(DecodeParams p) {
 
 template <typename T, int D>
 static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t s) {
-  const int nqg = (p.Hq / p.Hkv + 31) / 32;
-  const int grid = p.B * p.Hkv * nqg * p.splits;
+  const int grid = DecodePlan<D>::grid(p);
   hipLaunchKernelGGL((ssa_decode_kernel<T, D>), dim3(grid), dim3(DecodeCfg<D>::NW * 64), 0, s, p);
   if (p.splits > 1) hipLaunchKernelGGL((ssa_decode_merge_kernel<T, D>), dim3(p.B * p.Hq), dim3(128), 0, s, p);
   return hipGetLastError();

@@ -26,6 +26,7 @@
 
 #include "ssa_common.hpp"
 #include "ssa_launch.hpp"
+#include "ssa_plan.hpp"
 #include "ssa_tile.hpp"
 
 namespace ssa {
@@ -87,13 +88,12 @@ struct FwdTile {
 // iteration t - 2 (its buffer last held tile t - 4, whose V was last read in
 // iteration t - 3) and must be complete at the start of iteration t - 1.
 template <typename T, int D, bool CAUSAL, bool NPOS>
-__device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& sv, const int qb, const int b,
-                                            const int h, const int hk, char* smem) {
+__device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const FwdPlan<D, CAUSAL>& pl, char* smem) {
   typedef FwdTile<T, D> FT;
   typedef typename FT::v8 v8;
-  constexpr int BM = 256, BN = 64, NW = 8, NB = 4;
-  constexpr int TILE = BN * D * 2;  // one K (or V) tile
-  constexpr int BUF = 2 * TILE;     // K_t then V_t
+  using Plan = FwdPlan<D, CAUSAL>;
+  constexpr int BM = Plan::BM, BN = Plan::BN, NW = Plan::NW, NB = Plan::NB;
+  constexpr int TILE = Plan::TILE, BUF = Plan::BUF;
   constexpr int ND16 = D / 16, ND32 = D / 32;
   constexpr int PER = (BN / 32 * BlockLayout<D>::IPB + NW - 1) / NW;  // loads per matrix per wave
   constexpr int LPT = 2 * PER;                                       // loads per tile per wave
@@ -105,36 +105,23 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
   const RowBase<D> rb(l32, hh);
   const TrBase<D> tb(lane);
   const LoadLane llk(lane, wave, p.k.ss), llv(lane, wave, p.v.ss);
-  const int N = sv.N;
+  const SeqView& sv = pl.sv;
+  const int N = pl.N, b = pl.b, h = pl.h;
   const T* qg = static_cast<const T*>(p.q.ptr) + sv.off(p.q, b) + h * p.q.sh;
-  const char* kg = static_cast<const char*>(p.k.ptr) + (sv.off(p.k, b) + hk * p.k.sh) * 2;
-  const char* vg = static_cast<const char*>(p.v.ptr) + (sv.off(p.v, b) + hk * p.v.sh) * 2;
   T* og = static_cast<T*>(const_cast<void*>(p.o.ptr)) + sv.off(p.o, b) + h * p.o.sh;
 
   const float n = *p.n_ptr;
   const float c = p.scale * *p.b_ptr;  // u = c * |q.k|
-  const int q0 = qb * BM;
+  const int q0 = pl.qb * BM;
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
 
-  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int NT = (kv_end + BN - 1) / BN;  // tiles streamed by the workgroup
+  const int NT = pl.NT;  // tiles streamed by the workgroup
   // tiles this wave computes on, and the first of them that needs masks
   const int Tw = wq0 >= N ? 0 : (CAUSAL ? (min(N, wq0 + 32) + BN - 1) / BN : NT);
   const int nfull = min(Tw, CAUSAL ? min(wq0 / BN, N / BN) : N / BN);
 
-  auto load_tile = [&](int t) {
-    if (t >= NT) return;
-    const uint32_t kl = lds0 + (t & (NB - 1)) * BUF;
-    const int r0 = t * BN;
-    if (r0 + BN <= N) {
-      tile_load_pieces<D, BN, NW, false>(kg, p.k.ss, r0, N, kl, wave, llk);
-      tile_load_pieces<D, BN, NW, false>(vg, p.v.ss, r0, N, kl + TILE, wave, llv);
-    } else {
-      tile_load_pieces<D, BN, NW, true>(kg, p.k.ss, r0, N, kl, wave, llk);
-      tile_load_pieces<D, BN, NW, true>(vg, p.v.ss, r0, N, kl + TILE, wave, llv);
-    }
-  };
+  auto load_tile = [&](int t) { pl.load_tile(t, lds0, wave, llk, llv); };
 
   v8 qf[ND16];
 #pragma unroll
@@ -443,28 +430,19 @@ __device__ __forceinline__ void fwd_sp_body(const FwdParams& p, const SeqView& s
 
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(512) void ssa_fwd_kernel(FwdParams p) {
-  constexpr int BM = 256;
-  __shared__ __attribute__((aligned(1024))) char smem[4 * 2 * 64 * D * 2];
-  const int nqb = (p.N + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  // Logical order (head, sequence): each XCD's contiguous range holds a slice
-  // of heads of every sequence (balanced when packed sequences differ in
-  // length); query blocks heaviest (last) first within pairs of heads.
-  int hb, rank;
-  dispatch_order(L, gridDim.x / nqb, nqb, p.cu_seqlens ? 1 : kOrderGroup, hb, rank);
-  const int qb = nqb - 1 - rank;
-  const int b = hb % p.B, h = hb / p.B, hk = h / (p.Hq / p.Hkv);
-  const SeqView sv(p.cu_seqlens, p.T, p.N, b);
-  if (qb * BM >= sv.N) return;  // packed: past the end of a shorter document
+  using Plan = FwdPlan<D, CAUSAL>;
+  __shared__ __attribute__((aligned(1024))) char smem[Plan::LDS_BYTES];
+  const Plan pl(p, blockIdx.x, gridDim.x);
+  if (pl.empty()) return;  // packed: past the end of a shorter document
   if (*p.n_ptr >= 0.f)
-    fwd_sp_body<T, D, CAUSAL, true>(p, sv, qb, b, h, hk, smem);
+    fwd_sp_body<T, D, CAUSAL, true>(p, pl, smem);
   else
-    fwd_sp_body<T, D, CAUSAL, false>(p, sv, qb, b, h, hk, smem);
+    fwd_sp_body<T, D, CAUSAL, false>(p, pl, smem);
 }
 
 template <typename T, int D, bool CAUSAL>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-  const int grid = (p.N + 255) / 256 * p.B * p.Hq;
+  const int grid = FwdPlan<D, CAUSAL>::grid(p);
   hipLaunchKernelGGL((ssa_fwd_kernel<T, D, CAUSAL>), dim3(grid), dim3(512), 0, stream, p);
   return hipGetLastError();
 }

@@ -51,7 +51,7 @@ struct LoadLane {
   uint32_t off;   // r * row stride + half * 16, bytes
   uint32_t hoff;  // half * 16, bytes
   int r;          // row within the block
-  __device__ __forceinline__ LoadLane(int lane, int wave, int64_t ss) {
+  __host__ __device__ __forceinline__ LoadLane(int lane, int wave, int64_t ss) {
     const int pos = lane & 31, half = lane >> 5;
     r = pos ^ (4 * (2 * (wave & 1) + half));
     hoff = static_cast<uint32_t>(half * 16);
@@ -61,7 +61,7 @@ struct LoadLane {
   // r ^ 8 (c & 1).  A 1 KB piece covers chunks 2 cp and 2 cp + 1, so the
   // row a lane fetches depends on its half only, not on the wave.
   struct Swz8 {};
-  __device__ __forceinline__ LoadLane(int lane, int64_t ss, Swz8) {
+  __host__ __device__ __forceinline__ LoadLane(int lane, int64_t ss, Swz8) {
     const int pos = lane & 31, half = lane >> 5;
     r = pos ^ (8 * half);
     hoff = static_cast<uint32_t>(half * 16);
@@ -95,7 +95,7 @@ struct LoadLane {
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer descriptor: base address, stride 0, no bounds check in practice.
-__device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
+__host__ __device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   return i32x4_t{static_cast<int>(static_cast<uint32_t>(a)), static_cast<int>((a >> 32) & 0xffff), 0x7fffffff,
                  0x00020000};
@@ -171,9 +171,35 @@ __device__ __forceinline__ void buffer_store_b128_nt(const i32x4_t& rs, uint32_t
                : "memory");
 }
 
-template <int D, int ROWS, int NW, bool CLAMP>
-__device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
-                                                 const LoadLane& ll) {
+// The global-memory operations of the tile helpers below and of the kernels'
+// load / store plans (ssa_plan.hpp), as a policy: DeviceMem issues them with
+// the statements above.  The helpers and plans are __host__ __device__, so a
+// host program can replay them with a policy that records every address
+// instead (tests/host_addr: every workgroup, wave and lane of a problem).
+// `uniform` states that a value is wave-uniform (an SGPR on the device).
+struct DeviceMem {
+  __device__ __forceinline__ void load16(uint32_t lds, const i32x4_t& rs, uint32_t voff, int soff) const {
+    dma_buffer16<false>(lds, rs, voff, soff);
+  }
+  __device__ __forceinline__ void load16_nt(uint32_t lds, const i32x4_t& rs, uint32_t voff, int soff) const {
+    dma_buffer16<true>(lds, rs, voff, soff);
+  }
+  __device__ __forceinline__ void load16_global(uint32_t lds, const void* src) const { dma_global16(lds, src); }
+  __device__ __forceinline__ void load4_global(uint32_t lds, const void* src) const { dma_global4(lds, src); }
+  template <int OFF>
+  __device__ __forceinline__ void store16_nt(const i32x4_t& rs, uint32_t voff, int soff, u32x4 v) const {
+    buffer_store_b128_nt<OFF>(rs, voff, soff, v);
+  }
+  template <int OFF>
+  __device__ __forceinline__ void store16_nt_global(void* p, u32x4 v) const {
+    store_b128_nt<OFF>(p, v);
+  }
+  __device__ __forceinline__ int uniform(int x) const { return __builtin_amdgcn_readfirstlane(x); }
+};
+
+template <int D, int ROWS, int NW, bool CLAMP, typename Mem = DeviceMem>
+__host__ __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int row0, int nrows, uint32_t lds,
+                                                          int wave, const LoadLane& ll, const Mem& mem = Mem()) {
   using BL = BlockLayout<D>;
   constexpr int NINST = ROWS / 32 * BL::IPB;
   constexpr int PER = (NINST + NW - 1) / NW;
@@ -186,11 +212,11 @@ __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int 
     if (!CLAMP) {
       // descriptor base at row0 (scalar), per-lane row offset fixed for the
       // kernel (VGPR), block/chunk offset in soffset
-      dma_buffer16(lds + j * 1024, rs, ll.off, static_cast<int>(blk * 32 * ss * 2 + cp * 32));
+      mem.load16(lds + j * 1024, rs, ll.off, static_cast<int>(blk * 32 * ss * 2 + cp * 32));
     } else {
       int grow = row0 + blk * 32 + ll.r;
       grow = grow < nrows ? grow : nrows - 1;
-      dma_global16(lds + j * 1024, g + (static_cast<int64_t>(grow) * ss + cp * 16) * 2 + ll.hoff);
+      mem.load16_global(lds + j * 1024, g + (static_cast<int64_t>(grow) * ss + cp * 16) * 2 + ll.hoff);
     }
   }
 }
@@ -198,32 +224,33 @@ __device__ __forceinline__ void tile_load_pieces(const char* g, int64_t ss, int 
 // tile_load_pieces for a tile of full rows at byte soff0 of the buffer rs,
 // with 32-bit offsets (the caller keeps every byte of the tile below 2 GiB of
 // the descriptor base): one scalar add per piece, no 64-bit address math.
-template <int D, int ROWS, int NW>
-__device__ __forceinline__ void tile_load_pieces_off(const i32x4_t& rs, int soff0, int ss2, uint32_t lds, int wave,
-                                                     const LoadLane& ll) {
+template <int D, int ROWS, int NW, typename Mem = DeviceMem>
+__host__ __device__ __forceinline__ void tile_load_pieces_off(const i32x4_t& rs, int soff0, int ss2, uint32_t lds,
+                                                              int wave, const LoadLane& ll, const Mem& mem = Mem()) {
   using BL = BlockLayout<D>;
   constexpr int NINST = ROWS / 32 * BL::IPB;
   constexpr int PER = (NINST + NW - 1) / NW;
   // wave-uniform by construction; stated so that the offset is an SGPR
-  const int base = __builtin_amdgcn_readfirstlane(soff0);
+  const int base = mem.uniform(soff0);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int j = wave + NW * i;
     if (NINST % NW != 0 && j >= NINST) break;
     const int blk = j / BL::IPB, cp = j % BL::IPB;
-    dma_buffer16(lds + j * 1024, rs, ll.off, base + blk * 32 * ss2 + cp * 32);
+    mem.load16(lds + j * 1024, rs, ll.off, base + blk * 32 * ss2 + cp * 32);
   }
 }
 
-template <int D, int ROWS, int NW>
-__device__ __forceinline__ void tile_load_async(const void* gbase, int64_t ss, int row0, int nrows, uint32_t lds,
-                                                int wave, const LoadLane& ll) {
+template <int D, int ROWS, int NW, typename Mem = DeviceMem>
+__host__ __device__ __forceinline__ void tile_load_async(const void* gbase, int64_t ss, int row0, int nrows,
+                                                         uint32_t lds, int wave, const LoadLane& ll,
+                                                         const Mem& mem = Mem()) {
   static_assert(NW % 2 == 0 && BlockLayout<D>::IPB % 2 == 0, "chunk parity must be fixed per wave");
   const char* g = static_cast<const char*>(gbase);
   if (row0 + ROWS <= nrows)
-    tile_load_pieces<D, ROWS, NW, false>(g, ss, row0, nrows, lds, wave, ll);
+    tile_load_pieces<D, ROWS, NW, false>(g, ss, row0, nrows, lds, wave, ll, mem);
   else
-    tile_load_pieces<D, ROWS, NW, true>(g, ss, row0, nrows, lds, wave, ll);
+    tile_load_pieces<D, ROWS, NW, true>(g, ss, row0, nrows, lds, wave, ll, mem);
 }
 
 // Wait until at most N vector-memory instructions of this wave (direct tile
@@ -327,7 +354,7 @@ struct RowSwzLoad {
   uint32_t voff;  // lane's byte offset from a piece's first row
   int rsub;       // row within the piece (lane / 16)
   int chunk;      // chunk of that row the lane fetches
-  __device__ __forceinline__ RowSwzLoad(int lane, int64_t ss) {
+  __host__ __device__ __forceinline__ RowSwzLoad(int lane, int64_t ss) {
     rsub = lane >> 4;
     chunk = (lane & 15) ^ (4 * rsub);  // rows of a piece start at a multiple of 4: r & 3 = rsub
     voff = static_cast<uint32_t>(rsub * ss * 2 + chunk * 16);
@@ -337,9 +364,9 @@ struct RowSwzLoad {
 // Rows row0 .. row0 + ROWS - 1 (clamped to nrows - 1) of a [*, 128] matrix
 // with row stride `ss` elements into a RowSwz tile at `lds`: piece j (rows
 // 4 j .. 4 j + 3) from wave j % NW.
-template <int ROWS, int NW>
-__device__ __forceinline__ void rowswz_load(const char* g, int64_t ss, int row0, int nrows, uint32_t lds, int wave,
-                                            const RowSwzLoad& rl) {
+template <int ROWS, int NW, typename Mem = DeviceMem>
+__host__ __device__ __forceinline__ void rowswz_load(const char* g, int64_t ss, int row0, int nrows, uint32_t lds,
+                                                     int wave, const RowSwzLoad& rl, const Mem& mem = Mem()) {
   static_assert(ROWS % (4 * NW) == 0, "whole pieces per wave");
   constexpr int PER = ROWS / 4 / NW;
   if (row0 + ROWS <= nrows) {
@@ -347,7 +374,7 @@ __device__ __forceinline__ void rowswz_load(const char* g, int64_t ss, int row0,
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int j = wave + NW * i;
-      dma_buffer16(lds + j * 1024, rs, rl.voff, static_cast<int>(4 * j * ss * 2));
+      mem.load16(lds + j * 1024, rs, rl.voff, static_cast<int>(4 * j * ss * 2));
     }
   } else {
 #pragma unroll
@@ -355,7 +382,7 @@ __device__ __forceinline__ void rowswz_load(const char* g, int64_t ss, int row0,
       const int j = wave + NW * i;
       int row = row0 + 4 * j + rl.rsub;
       row = row < nrows ? row : nrows - 1;
-      dma_global16(lds + j * 1024, g + (static_cast<int64_t>(row) * ss + rl.chunk * 8) * 2);
+      mem.load16_global(lds + j * 1024, g + (static_cast<int64_t>(row) * ss + rl.chunk * 8) * 2);
     }
   }
 }
@@ -404,12 +431,13 @@ __device__ __forceinline__ void wait_lgkm() {
 // 32 consecutive fp32 values of each of two vectors (rows row0.. of `a` and of
 // `b`, clamped to nrows - 1) into 256 bytes of LDS at `lds`: a first, then b.
 // One global_load_lds_dword issued by the calling wave.
-__device__ __forceinline__ void pair32_load_async(const float* a, const float* b, int row0, int nrows, uint32_t lds,
-                                                  int lane) {
+template <typename Mem = DeviceMem>
+__host__ __device__ __forceinline__ void pair32_load_async(const float* a, const float* b, int row0, int nrows,
+                                                           uint32_t lds, int lane, const Mem& mem = Mem()) {
   int r = row0 + (lane & 31);
   r = r < nrows ? r : nrows - 1;
   const float* src = (lane < 32 ? a : b) + r;
-  dma_global4(lds, src);
+  mem.load4_global(lds, src);
 }
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
