@@ -250,6 +250,64 @@ def measured_counters(config):
     return out
 
 
+def roofline_of(kernels: dict, alg_io: dict, peak_flops: float, fp32: bool, config: str) -> dict:
+    """Rates, fractions and the bounding roof of every kernel (in place), and
+    the `roofline` object of the dominant (longest) kernel.
+
+    A kernel priced in FLOPs is compute-bound when its intensity (FLOP per HBM
+    byte: measured traffic where a profile exists, else its algorithmic bytes)
+    lies above the ridge of the two roofs, HBM-bound otherwise; an HBM-bound
+    one is then rated by its algorithmic bytes (inputs read once, outputs
+    written once).  Kernels priced in bytes are HBM-bound."""
+    ridge = peak_flops * 1e12 / (PEAK_HBM_GBPS * 1e9)  # FLOP per HBM byte where the two roofs meet
+    for name, kd in kernels.items():
+        if "alg_flop" in kd:
+            kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
+            kd["frac_peak"] = kd["tflops"] / peak_flops
+            if fp32:
+                kd["frac_valu_peak"] = kd["tflops"] / PEAK_FP32_VALU_TFLOPS
+            nbytes = kd.get("hbm_bytes") or alg_io.get(name)
+            if nbytes:
+                kd["intensity_flop_per_byte"] = kd["alg_flop"] / nbytes
+                compute = kd["intensity_flop_per_byte"] > ridge
+            else:
+                compute = True
+            kd["bound"] = ("valu" if fp32 else "mfma") if compute else "hbm"
+            if not compute and alg_io.get(name):
+                kd["alg_bytes_io"] = alg_io[name]
+                kd["gbps"] = alg_io[name] / (kd["avg_ms"] * 1e-3) / 1e9
+                kd["frac_hbm_peak"] = kd["gbps"] / PEAK_HBM_GBPS
+        if "alg_bytes" in kd:
+            kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
+            kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
+            kd["bound"] = "hbm"
+    dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
+    kd = kernels[dominant]
+    if kd.get("bound") in ("mfma", "valu"):
+        roofline = {"kernel": dominant, "bound": kd["bound"], "achieved": kd["tflops"], "peak": peak_flops,
+                    "unit": "TFLOP/s", "frac": kd["tflops"] / peak_flops, "traffic": kd.get("hbm_bytes"),
+                    "avg_launch_ms": kd["avg_ms"]}
+    else:
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": kd["gbps"], "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": kd.get("hbm_bytes"),
+                    "avg_launch_ms": kd["avg_ms"]}
+        if "tflops" in kd:
+            roofline["tflops"] = kd["tflops"]
+    cn = kd.get("counters")
+    if cn and "alg_flop" in kd:
+        # The SSA element work is the co-bound: the counters say what limits
+        # the kernel below its roofline (matrix-core and VALU busy fractions
+        # per SIMD at the measured clock, instructions per MFMA, and the share
+        # of wave time spent waiting).
+        roofline["co_bound"] = {
+            "mfma_busy": cn["mfma_busy"], "valu_busy": cn["valu_busy"],
+            "valu_per_mfma": cn["valu_per_mfma"], "trans_per_mfma": cn["trans_per_mfma"],
+            "salu_per_mfma": cn["salu_per_mfma"], "wait_frac": cn["wait_any"] + cn["wait_dep"],
+            "clock_ghz": cn["clock_ghz"], "limiter": limiter_from_counters(cn),
+            "source": f"profiles/ssa_counters_{config}.md", "profile_build": cn.get("build")}
+    return roofline
+
+
 def limiter_from_counters(cn):
     """What the counter row says holds a kernel below its compute roof: a unit
     busy >= 80 % of the SIMD-cycles is saturated; otherwise the waves' waiting
@@ -502,50 +560,10 @@ def main():
     tq, tkv, rows_b = B * Hq * S * D * esize, B * Hkv * S * D * esize, B * Hq * S * 4
     alg_io = {"ssa_fwd_kernel": 2 * tq + 2 * tkv + rows_b,
               "ssa_bwd_dkdv_kernel": 2 * tq + 4 * tkv + 2 * rows_b + ds_bytes}
-    ridge = peak_flops * 1e12 / (PEAK_HBM_GBPS * 1e9)  # FLOP per HBM byte where the two roofs meet
     for name, kd in kernels.items():
         kd["hbm_bytes"] = traffic.get(name)
         kd["counters"] = counters.get(hip_name.get(name, name))
-        if "alg_flop" in kd:
-            kd["tflops"] = kd["alg_flop"] / (kd["avg_ms"] * 1e-3) / 1e12
-            kd["frac_peak"] = kd["tflops"] / peak_flops
-            if dtype == torch.float32:
-                kd["frac_valu_peak"] = kd["tflops"] / PEAK_FP32_VALU_TFLOPS
-            # the roof that bounds it: compute when its intensity (FLOP per HBM
-            # byte, measured traffic where a profile exists) is above the ridge
-            nbytes = kd["hbm_bytes"] or alg_io.get(name)
-            if nbytes:
-                kd["intensity_flop_per_byte"] = kd["alg_flop"] / nbytes
-                compute = kd["intensity_flop_per_byte"] > ridge
-            else:
-                compute = True
-            kd["bound"] = ("valu" if dtype == torch.float32 else "mfma") if compute else "hbm"
-        if "alg_bytes" in kd:
-            kd["gbps"] = kd["alg_bytes"] / (kd["avg_ms"] * 1e-3) / 1e9
-            kd["frac_peak"] = kd["gbps"] / PEAK_HBM_GBPS
-            kd["bound"] = "hbm"
-    dominant = max(kernels, key=lambda k_: kernels[k_]["avg_ms"])
-    kd = kernels[dominant]
-    if kd.get("bound") in ("mfma", "valu"):
-        roofline = {"kernel": dominant, "bound": kd["bound"], "achieved": kd["tflops"], "peak": peak_flops,
-                    "unit": "TFLOP/s", "frac": kd["tflops"] / peak_flops, "traffic": kd["hbm_bytes"],
-                    "avg_launch_ms": kd["avg_ms"]}
-        cn = kd.get("counters")
-        if cn:
-            # The SSA element work is the co-bound: the counters say what limits
-            # the kernel below the MFMA roofline (matrix-core and VALU busy
-            # fractions per SIMD at the measured clock, instructions per MFMA,
-            # and the share of wave time spent waiting).
-            roofline["co_bound"] = {
-                "mfma_busy": cn["mfma_busy"], "valu_busy": cn["valu_busy"],
-                "valu_per_mfma": cn["valu_per_mfma"], "trans_per_mfma": cn["trans_per_mfma"],
-                "salu_per_mfma": cn["salu_per_mfma"], "wait_frac": cn["wait_any"] + cn["wait_dep"],
-                "clock_ghz": cn["clock_ghz"], "limiter": limiter_from_counters(cn),
-                "source": f"profiles/ssa_counters_{args.config}.md", "profile_build": cn.get("build")}
-    else:
-        roofline = {"kernel": dominant, "bound": "hbm", "achieved": kd["gbps"], "peak": PEAK_HBM_GBPS,
-                    "unit": "GB/s", "frac": kd["gbps"] / PEAK_HBM_GBPS, "traffic": kd["hbm_bytes"],
-                    "avg_launch_ms": kd["avg_ms"]}
+    roofline = roofline_of(kernels, alg_io, peak_flops, dtype == torch.float32, args.config)
 
     fwd_ms = kernels["ssa_fwd_kernel"]["avg_ms"]
     bwd_ms = sum(kernels[f"ssa_bwd_{s}_kernel"]["avg_ms"] for s in BackwardLaunch.STAGES)

@@ -84,3 +84,35 @@ def test_committed_profiles_parse():
         assert 0.0 <= d["mfma_busy"] <= 1.0 and 0.0 <= d["valu_busy"] <= 1.0
     t = bench.measured_traffic("s4096")
     assert {"ssa_fwd_kernel", "ssa_bwd_preprocess_kernel", "ssa_bwd_dkdv_kernel", "ssa_bwd_dq_kernel"} <= set(t)
+
+
+def test_roofline_of_each_bound():
+    """The roofline object for each kind of dominant kernel: a FLOP-priced one
+    above the ridge (MFMA roof), a FLOP-priced one below it (rated in GB/s by
+    its algorithmic bytes: the GQA D = 64 dK/dV, whose dS' workspace write
+    lowers its intensity), and a byte-priced one."""
+    ridge = bench.PEAK_BF16_TFLOPS * 1e12 / (bench.PEAK_HBM_GBPS * 1e9)
+    # above the ridge: 550 GFLOP over 1.5 GB (measured traffic)
+    k = {"ssa_bwd_dkdv_kernel": {"avg_ms": 0.8, "alg_flop": 5.5e11, "hbm_bytes": 1.5e9},
+         "ssa_fwd_kernel": {"avg_ms": 0.3, "alg_flop": 2.75e11}}
+    r = bench.roofline_of(k, {"ssa_bwd_dkdv_kernel": 2.4e9}, bench.PEAK_BF16_TFLOPS, False, "s4096")
+    assert 5.5e11 / 1.5e9 > ridge
+    assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["kernel"] == "ssa_bwd_dkdv_kernel"
+    assert r["achieved"] == pytest.approx(5.5e11 / 0.8e-3 / 1e12)
+    assert r["frac"] == pytest.approx(r["achieved"] / bench.PEAK_BF16_TFLOPS)
+    # below the ridge, no measured traffic: intensity from the algorithmic bytes
+    k = {"ssa_bwd_dkdv_kernel": {"avg_ms": 0.95, "alg_flop": 5.5e11},
+         "ssa_bwd_dq_kernel": {"avg_ms": 0.4, "alg_flop": 1.4e11, "alg_bytes": 2.2e9}}
+    r = bench.roofline_of(k, {"ssa_bwd_dkdv_kernel": 2.4e9}, bench.PEAK_BF16_TFLOPS, False, "gqa_d64")
+    assert 5.5e11 / 2.4e9 < ridge
+    assert r["bound"] == "hbm" and r["unit"] == "GB/s"
+    assert r["achieved"] == pytest.approx(2.4e9 / 0.95e-3 / 1e9)
+    assert r["frac"] == pytest.approx(r["achieved"] / bench.PEAK_HBM_GBPS)
+    assert r["tflops"] == pytest.approx(5.5e11 / 0.95e-3 / 1e12)
+    assert k["ssa_bwd_dq_kernel"]["bound"] == "hbm"
+    # a byte-priced dominant kernel
+    k = {"ssa_bwd_dq_kernel": {"avg_ms": 0.4, "alg_flop": 1.4e11, "alg_bytes": 2.2e9},
+         "ssa_fwd_kernel": {"avg_ms": 0.3, "alg_flop": 2.75e11}}
+    r = bench.roofline_of(k, {}, bench.PEAK_BF16_TFLOPS, False, "s4096")
+    assert r["kernel"] == "ssa_bwd_dq_kernel" and r["bound"] == "hbm"
+    assert r["achieved"] == pytest.approx(2.2e9 / 0.4e-3 / 1e9)
