@@ -171,6 +171,17 @@ def _ssa_name(kernel_name):
     return m.group(1) if m else None
 
 
+def dkdv_hip_name(D: int, dtype: str) -> str:
+    """The HIP kernel the library runs for the dK/dV stage (csrc/ssa_bwd.hip
+    use_dkdv2w): the two-wave kernel at head dim 128 for bf16 / fp16 unless
+    SSA_DKDV2W=0, at every head dim with SSA_DKDV2W=1."""
+    if dtype == "fp32":
+        return "ssa_bwd_dkdv_f32_kernel"
+    e = os.environ.get("SSA_DKDV2W", "")
+    two = e[:1] == "1" if e[:1] in ("0", "1") else D == 128
+    return "ssa_bwd_dkdv2w_kernel" if two else "ssa_bwd_dkdv_kernel"
+
+
 def trace_summary(trace_csv):
     """Markdown table of the SSA kernels in a rocprofv3 --kernel-trace CSV."""
     import statistics
@@ -212,6 +223,7 @@ def traffic_summary(fetch_csv, write_csv, config="s4096"):
             name = _ssa_name(k)
             if name:
                 name = "ssa_bwd_dq_kernel" if name.startswith("ssa_bwd_dq") else name
+                name = "ssa_bwd_dkdv_kernel" if name.startswith("ssa_bwd_dkdv") else name
                 vals.setdefault(name, {})[which] = v * scale * 1024 / 1e6
         vals.setdefault("_scale", {})[which] = scale
     lines = [f"Calibration: FETCH_SIZE x{vals['_scale']['fetch']:.4f}, WRITE_SIZE x{vals['_scale']['write']:.4f} "
@@ -555,6 +567,7 @@ def main():
     traffic = measured_traffic(args.config) if args.dtype == "bf16" else {}
     counters = measured_counters(args.config) if args.dtype == "bf16" else {}
     hip_name = {"ssa_bwd_dq_kernel": "ssa_bwd_dq_ds_kernel" if ds_bytes else "ssa_bwd_dq_kernel",
+                "ssa_bwd_dkdv_kernel": dkdv_hip_name(D, args.dtype),
                 "ssa_bwd_reduce_kernel": "ssa_reduce_partials_kernel"}
     # algorithmic HBM bytes of the FLOP-priced kernels (inputs read once, outputs written once)
     tq, tkv, rows_b = B * Hq * S * D * esize, B * Hkv * S * D * esize, B * Hq * S * 4
@@ -564,6 +577,7 @@ def main():
         kd["hbm_bytes"] = traffic.get(name)
         kd["counters"] = counters.get(hip_name.get(name, name))
     roofline = roofline_of(kernels, alg_io, peak_flops, dtype == torch.float32, args.config)
+    roofline["hip_kernel"] = hip_name.get(roofline["kernel"], roofline["kernel"])
 
     fwd_ms = kernels["ssa_fwd_kernel"]["avg_ms"]
     bwd_ms = sum(kernels[f"ssa_bwd_{s}_kernel"]["avg_ms"] for s in BackwardLaunch.STAGES)

@@ -11,10 +11,14 @@ buffer stores of csrc/ssa_tile.hpp) is not protected against:
   followed by a vector-memory instruction that reads that SGPR (descriptor,
   soffset, saddr): 5 wait states are required;
 * an SALU write of M0 followed by an LDS DMA (buffer_* ... lds,
-  global_load_lds_*), which reads M0: 1 wait state.
+  global_load_lds_*), which reads M0: 1 wait state;
+* a vector-memory store of more than 8 bytes (global_/buffer_/flat_/scratch_
+  store_dwordx3, _dwordx4) followed by a VALU instruction that writes one of
+  its data VGPRs: 2 wait states on gfx940 and later (the store reads its data
+  after issue, so an early overwrite changes what is stored).
 
 With fewer, the memory instruction can read the register's previous value
-and so access a wrong address.  ``scan_asm`` walks a device .s file in
+and so access a wrong address (or, for the store data, store the new value).  ``scan_asm`` walks a device .s file in
 program order (a label does not reset the window, so fall-through paths are
 covered) and returns every site with fewer wait states than required.
 
@@ -39,6 +43,10 @@ VMEM = re.compile(r"^(buffer_|global_|flat_|scratch_)")
 LDS_DMA = re.compile(r"^(buffer_\w+.*\blds\b|global_load_lds_)")
 VALU_SGPR_WAIT = 5
 M0_LDS_DMA_WAIT = 1
+STORE_DATA_WAIT = 2
+WIDE_STORE = re.compile(r"^(global|buffer|flat|scratch)_store_dwordx[34]$")
+# VALU instructions whose first operand is not a VGPR destination
+_VALU_NO_VDST = re.compile(r"^v_(readlane|readfirstlane|cmp|cmpx|nop)")
 ACC_MFMA_SRC_WAIT = 2   # VALU write of an MFMA source -> MFMA
 ACC_READ_WAIT = 19      # XDL write (up to 16 passes) -> any other access of its result
 
@@ -76,7 +84,7 @@ def _salu_m0_def(parts: list) -> bool:
 def scan_asm(text: str) -> list:
     """Hazard sites of one device assembly file: (function, wait states, needed, instruction)."""
     func = None
-    window = []  # most recent first-to-last: (sgpr defs by VALU, writes m0 by SALU)
+    window = []  # most recent first-to-last: (sgpr defs by VALU, writes m0 by SALU, wide-store data VGPRs)
     sites = []
     for raw in text.split("\n"):
         m = re.match(r"^(_Z\S+|[A-Za-z_]\w*):", raw)
@@ -89,8 +97,16 @@ def scan_asm(text: str) -> list:
         parts = s.replace(",", " ").split()
         if parts[0] == "s_nop":
             n = int(parts[1], 0) + 1 if len(parts) > 1 else 1
-            window.extend([(set(), False)] * n)
+            window.extend([(set(), False, set())] * n)
         else:
+            if parts[0].startswith("v_") and not _VALU_NO_VDST.match(parts[0]) and len(parts) > 1:
+                vdst = _vregs(parts[1])
+                for ws, (_, _, data) in enumerate(reversed(window)):
+                    if ws >= STORE_DATA_WAIT:
+                        break
+                    if data & vdst:
+                        sites.append((func, ws, STORE_DATA_WAIT, s))
+                        break
             if VMEM.match(parts[0]):
                 used = set()
                 for t in parts[1:]:
@@ -100,20 +116,23 @@ def scan_asm(text: str) -> list:
                 # each rule on its own: the most recent VALU write of an SGPR the
                 # instruction reads, and the most recent SALU write of M0
                 vgpr_sgpr = used - {"m0"}
-                for ws, (defs, _) in enumerate(reversed(window)):
+                for ws, (defs, _, _) in enumerate(reversed(window)):
                     if ws >= VALU_SGPR_WAIT:
                         break
                     if defs & vgpr_sgpr:
                         sites.append((func, ws, VALU_SGPR_WAIT, s))
                         break
                 if "m0" in used:
-                    for ws, (_, m0) in enumerate(reversed(window)):
+                    for ws, (_, m0, _) in enumerate(reversed(window)):
                         if ws >= M0_LDS_DMA_WAIT:
                             break
                         if m0:
                             sites.append((func, ws, M0_LDS_DMA_WAIT, s))
                             break
-            window.append((_valu_sgpr_defs(parts), _salu_m0_def(parts)))
+            data = set()
+            if WIDE_STORE.match(parts[0]) and len(parts) > 2:
+                data = _vregs(parts[1] if parts[0].startswith("buffer_") else parts[2])
+            window.append((_valu_sgpr_defs(parts), _salu_m0_def(parts), data))
         del window[:-8]
     return sites
 

@@ -91,29 +91,6 @@ __device__ __forceinline__ V4 lds_tr4(uint32_t addr) {
                                     (__attribute__((address_space(3))) bf16x4_t*)(uintptr_t)addr));
 }
 
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 15]; larger n wait for all.
-__device__ __forceinline__ void wait_vm_dyn(int n) {
-  switch (n) {
-    case 1: wait_vm<1>(); break;
-    case 2: wait_vm<2>(); break;
-    case 3: wait_vm<3>(); break;
-    case 4: wait_vm<4>(); break;
-    case 5: wait_vm<5>(); break;
-    case 6: wait_vm<6>(); break;
-    case 7: wait_vm<7>(); break;
-    case 8: wait_vm<8>(); break;
-    case 9: wait_vm<9>(); break;
-    case 10: wait_vm<10>(); break;
-    case 11: wait_vm<11>(); break;
-    case 12: wait_vm<12>(); break;
-    case 13: wait_vm<13>(); break;
-    case 14: wait_vm<14>(); break;
-    case 15: wait_vm<15>(); break;
-    default: wait_vm<0>(); break;
-  }
-}
-
-
 // MFMA schedule of a slot: item index -> kind and tick.  Items in order:
 //   H1: dV/dK of step j - 1, query half 1 (2 NDB: dV, dK per column block)
 //   B3: S/dP block 3 of step j (2 NKS: S, dP per k-step)

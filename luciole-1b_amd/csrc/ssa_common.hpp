@@ -244,4 +244,36 @@ constexpr float kRescaleTau = 8.0f;
 // the fp32 sums far from overflow while M = m + log2(l) stays exact.
 constexpr float kPsumLimit = 1048576.0f;
 
+// dn, db = fixed-order sums of the per-workgroup partials: threads 0 .. 255
+// of the calling workgroup Kahan-sum strided slices, then a fixed tree; every
+// thread of the workgroup reaches the barriers.
+__device__ __forceinline__ void reduce_partials_body(const float* partials, int64_t count, float* dn, float* db,
+                                                     float (*sh)[256], int tid) {
+  if (tid < 256) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const float* src = partials + w * count;
+      float acc = 0.f, comp = 0.f;
+      for (int64_t i = tid; i < count; i += 256) {
+        const float y = src[i] - comp, t = acc + y;
+        comp = (t - acc) - y;
+        acc = t;
+      }
+      sh[w][tid] = acc;
+    }
+  }
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (tid < stride) {
+      sh[0][tid] += sh[0][tid + stride];
+      sh[1][tid] += sh[1][tid + stride];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    *dn = sh[0][0];
+    *db = sh[1][0];
+  }
+}
+
 }  // namespace ssa

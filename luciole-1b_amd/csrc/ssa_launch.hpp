@@ -15,6 +15,8 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, bool causal, hi
 // dK/dV with two waves per SIMD (ssa_bwd_dkdv2w.hip): bf16 / fp16, D in {32, 64, 128}.
 hipError_t launch_bwd_dkdv2w(const BwdParams& p, int dtype, int D, bool causal, bool off32, hipStream_t stream);
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
+// dQ from the dS' workspace (ssa_bwd_dq.hip): bf16 / fp16, D in {32, 64, 128}.
+hipError_t launch_bwd_dq_ds(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
 hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t stream);

@@ -476,10 +476,12 @@ constexpr int dq_ds_waves() {
   return D >= 64 ? 8 : 4;
 }
 
-template <int D, bool CAUSAL, int NW>
+// Ring depths: NK K buffers loaded PFK steps ahead, NDS dS' stages loaded
+// PFD steps ahead.
+template <int D, bool CAUSAL, int NW, int NK_ = 2, int PFK_ = 1, int NDS_ = 3, int PFD_ = 2>
 struct DqDsLoads {
   static constexpr int BM = 32 * NW, BN = 64;
-  static constexpr int NK = 2, PFK = 1, NDS = 3, PFD = 2;
+  static constexpr int NK = NK_, PFK = PFK_, NDS = NDS_, PFD = PFD_;
   static constexpr int KTILE = BN * D * 2;
   static constexpr int DSTAGE = NW * 4096;  // NW waves x 4 dS' tiles
   static constexpr int LDS_BYTES = NK * KTILE + NDS * DSTAGE;

@@ -154,18 +154,20 @@ __device__ __forceinline__ void buffer_store_b64(const i32x4_t& rs, uint32_t vof
 // 16 bytes per lane with the non-temporal (streaming) cache policy, one
 // vector-memory instruction each (as store_b64 / buffer_store_b64): for data
 // written once and read back once by a later kernel, so that it does not
-// evict reused tiles from L2.  A store of more than 8 bytes must not have its
-// data registers overwritten by the very next instruction: the trailing
-// s_nop 0 keeps that wait state inside the statement.
+// evict reused tiles from L2.  On gfx940 and later a store of more than 8
+// bytes needs 2 wait states before a VALU instruction overwrites its data
+// registers (the compiler pads only the stores it sees): the trailing s_nop 1
+// keeps them inside the statement, and the build's assembly scan
+// (SSA/_hazards.py) rejects any store whose data is overwritten sooner.
 template <int OFF>
 __device__ __forceinline__ void store_b128_nt(void* p, u32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off offset:%2 nt\n\ts_nop 0" : : "v"(reinterpret_cast<uint64_t>(p)),
+  asm volatile("global_store_dwordx4 %0, %1, off offset:%2 nt\n\ts_nop 1" : : "v"(reinterpret_cast<uint64_t>(p)),
                "v"(v), "i"(OFF)
                : "memory");
 }
 template <int OFF>
 __device__ __forceinline__ void buffer_store_b128_nt(const i32x4_t& rs, uint32_t voff, int soff, u32x4 v) {
-  asm volatile("s_nop 4\n\tbuffer_store_dwordx4 %0, %1, %2, %3 offen offset:%4 nt\n\ts_nop 0"
+  asm volatile("s_nop 4\n\tbuffer_store_dwordx4 %0, %1, %2, %3 offen offset:%4 nt\n\ts_nop 1"
                :
                : "v"(v), "v"(voff), "s"(rs), "s"(soff), "i"(OFF)
                : "memory");
@@ -260,6 +262,44 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31]; larger n wait for all.
+__device__ __forceinline__ void wait_vm_dyn(int n) {
+  switch (n) {
+    case 1: wait_vm<1>(); break;
+    case 2: wait_vm<2>(); break;
+    case 3: wait_vm<3>(); break;
+    case 4: wait_vm<4>(); break;
+    case 5: wait_vm<5>(); break;
+    case 6: wait_vm<6>(); break;
+    case 7: wait_vm<7>(); break;
+    case 8: wait_vm<8>(); break;
+    case 9: wait_vm<9>(); break;
+    case 10: wait_vm<10>(); break;
+    case 11: wait_vm<11>(); break;
+    case 12: wait_vm<12>(); break;
+    case 13: wait_vm<13>(); break;
+    case 14: wait_vm<14>(); break;
+    case 15: wait_vm<15>(); break;
+    case 16: wait_vm<16>(); break;
+    case 17: wait_vm<17>(); break;
+    case 18: wait_vm<18>(); break;
+    case 19: wait_vm<19>(); break;
+    case 20: wait_vm<20>(); break;
+    case 21: wait_vm<21>(); break;
+    case 22: wait_vm<22>(); break;
+    case 23: wait_vm<23>(); break;
+    case 24: wait_vm<24>(); break;
+    case 25: wait_vm<25>(); break;
+    case 26: wait_vm<26>(); break;
+    case 27: wait_vm<27>(); break;
+    case 28: wait_vm<28>(); break;
+    case 29: wait_vm<29>(); break;
+    case 30: wait_vm<30>(); break;
+    case 31: wait_vm<31>(); break;
+    default: wait_vm<0>(); break;
+  }
 }
 
 // A VGPR copy of x that the compiler cannot re-associate with later

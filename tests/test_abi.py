@@ -458,6 +458,27 @@ def test_hazard_scan_flags_short_waits():
     assert sites(far) == []
 
 
+def test_hazard_scan_flags_store_data_overwrite():
+    """The store-data rule: a VALU write of a data VGPR of a preceding
+    16-byte store needs 2 wait states (global data is the second operand,
+    buffer data the first); 8-byte stores, SGPR-destination VALU forms and
+    writes of other registers are not hazards."""
+    from SSA import _hazards
+
+    def sites(body):
+        return [s[1:3] for s in _hazards.scan_asm("_Zk:\n" + "\n".join("\t" + ln for ln in body))]
+
+    g = "global_store_dwordx4 v[10:11], v[4:7], off offset:16 nt"
+    assert sites([g, "s_nop 0", "v_bitop3_b32 v4, v3, v186, 3 bitop3:0x6c"]) == [(1, 2)]
+    assert sites([g, "v_mov_b32_e32 v7, 0"]) == [(0, 2)]
+    assert sites([g, "s_nop 1", "v_mov_b32_e32 v7, 0"]) == []
+    assert sites([g, "s_nop 0", "v_mov_b32_e32 v10, 0"]) == []  # the address, not the data
+    assert sites([g, "v_readfirstlane_b32 s4, v5", "v_cmp_gt_i32_e64 s[2:3], v4, v6"]) == []
+    b = "buffer_store_dwordx4 v[20:23], v2, s[8:11], s4 offen offset:512 nt"
+    assert sites([b, "s_nop 0", "v_add_u32_e32 v21, 1, v21"]) == [(1, 2)]
+    assert sites(["global_store_dwordx2 v[10:11], v[4:5], off", "v_mov_b32_e32 v4, 0"]) == []
+
+
 def test_agpr_scan_follows_every_path():
     """SSA/_hazards.py's check of the inline-assembly AGPR accumulations:
     in-place form after its own s_nop, and no other access to the block

@@ -1,10 +1,13 @@
-"""GPU parity of the two-waves-per-SIMD dK/dV kernel (csrc/ssa_bwd_dkdv2w.hip).
+"""GPU parity of both dK/dV kernels at every head dim: the two-waves-per-SIMD
+kernel (csrc/ssa_bwd_dkdv2w.hip, the default at head dim 128) and the
+single-wave kernel (csrc/ssa_bwd.hip, the default at 32 and 64), each forced
+with SSA_DKDV2W=1 / =0 at launch time, so that the kernel the library does
+not pick for a head dim stays tested too.
 
-The library runs it instead of the default dK/dV kernel when SSA_DKDV2W=1 is
-set at launch time.  Same oracle and bars as test_gpu_parity: head dims 32-128,
-bf16 / fp16, causal / non-causal, MHA / GQA, both backward paths (its dS'
-tiles feed the unchanged dQ pass), sequence lengths that are not multiples of
-the kernel's 64-query step or 128-key block, the divergent-layer n = -302,
+Same oracle and bars as test_gpu_parity: head dims 32-128, bf16 / fp16,
+causal / non-causal, MHA / GQA, both backward paths (their dS' tiles feed
+the same dQ pass), sequence lengths that are not multiples of the kernels'
+query steps or 128-key blocks, the divergent-layer n = -302,
 Megatron-strided inputs, bitwise determinism, and packed sequences.
 """
 
@@ -22,10 +25,10 @@ from parity_util import assert_parity
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
-def dkdv2w():
+@pytest.fixture(params=["1", "0"], ids=["2w", "1w"])
+def dkdv2w(request):
     old = os.environ.get("SSA_DKDV2W")
-    os.environ["SSA_DKDV2W"] = "1"
+    os.environ["SSA_DKDV2W"] = request.param
     yield
     if old is None:
         del os.environ["SSA_DKDV2W"]
