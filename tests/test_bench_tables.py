@@ -79,7 +79,9 @@ def test_trace_summary(tmp_path):
 def test_committed_profiles_parse():
     """The profiles bench.py reads for its JSON line parse into every kernel of the step."""
     c = bench.measured_counters("s4096")
-    assert {"ssa_fwd_kernel", "ssa_bwd_dkdv_kernel", "ssa_bwd_dq_ds_kernel"} <= set(c)
+    # the dK/dV stage under the HIP kernel name the library runs at this head dim
+    assert {"ssa_fwd_kernel", bench.dkdv_hip_name(128, "bf16"), "ssa_bwd_dq_ds_kernel"} <= set(c)
+    assert bench.dkdv_hip_name(64, "bf16") in bench.measured_counters("gqa_d64")
     for d in c.values():
         assert 0.0 <= d["mfma_busy"] <= 1.0 and 0.0 <= d["valu_busy"] <= 1.0
     t = bench.measured_traffic("s4096")
