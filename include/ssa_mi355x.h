@@ -45,7 +45,7 @@ enum {
                               /* B * Hq * ceil(seqlen / 128) <= 2^28, and query   */
                               /* rows B * Hq * seqlen (packed: Hq * total_tokens) */
                               /* <= INT32_MAX; decode: capacity <= 2^30          */
-  SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128 (fp32: also 16)  */
+  SSA_ERR_HEAD_DIM = 3,       /* head_dim not one of 32, 64, 128, 256 (fp32: 16)  */
   SSA_ERR_DTYPE = 4,          /* dtype not an SSA_DTYPE_* (decode: bf16 / fp16)   */
   SSA_ERR_ALIGNMENT = 5,      /* layout: base pointer not 16-byte aligned, a      */
                               /* stride negative or not a multiple of 8, or the   */
@@ -58,12 +58,15 @@ enum {
 
 /*
  * Element types of q/k/v/out/dout/dq/dk/dv.  bf16 / fp16 run on the MFMA
- * kernels (head dims 32, 64, 128).  fp32 -- the reference's fp32-operand path
- * (training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:766-772, 819-825)
- * -- runs on fp32 vector-ALU kernels (head dims 16, 32, 64, 128) that keep
- * every product in fp32: full precision, a fraction of the bf16 throughput;
- * with it the dS' workspace is not used (dq recomputes the scores) and the
- * decode step is not offered.
+ * kernels at head dims 32, 64, 128.  fp32 -- the reference's fp32-operand
+ * path (training/train/train_ssa_triton/SSA/ssa_triton_kernel.py:766-772,
+ * 819-825) -- runs on fp32 vector-ALU kernels (head dims 16, 32, 64, 128,
+ * 256) that keep every product in fp32: full precision, a fraction of the
+ * bf16 throughput.  bf16 / fp16 at head dim 256 (the reference takes every
+ * power-of-two head dim, ssa_triton_kernel.py:761-764) run on the same
+ * vector-ALU kernels, elements widened to fp32 on load.  On the vector-ALU
+ * kernels the dS' workspace is not used (dq recomputes the scores); the
+ * decode step takes bf16 / fp16 at head dims 32, 64, 128.
  */
 enum { SSA_DTYPE_BF16 = 0, SSA_DTYPE_FP16 = 1, SSA_DTYPE_FP32 = 2 };
 
@@ -112,7 +115,9 @@ typedef struct ssa_bwd_args {
                            set, dkdv stores dS' there and dq reads it back, so
                            both steps must get the same pointer.  Packed
                            sequences (ssa_varlen_bwd) need
-                           ssa_varlen_bwd_ds_workspace_bytes() bytes. */
+                           ssa_varlen_bwd_ds_workspace_bytes() bytes.  The
+                           vector-ALU kernels (fp32; head dim 256) ignore it:
+                           their dq always recomputes. */
 } ssa_bwd_args;
 
 /* Library ABI version (SSA_ABI_VERSION). */

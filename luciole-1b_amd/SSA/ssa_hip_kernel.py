@@ -140,6 +140,14 @@ def ssa_flash_attn_forward(q, k, v, softmax_scale, ssa_n, ssa_b, causal=True):
     return out, m
 
 
+def _has_ds_path(dtype: torch.dtype, head_dim: int) -> bool:
+    """Whether the backward kernels for ``dtype`` / ``head_dim`` can use a dS'
+    workspace: the matrix-core kernels (bf16 / fp16 at head dims up to 128)
+    can; the fp32-arithmetic vector-ALU kernels (fp32, and head dim 256) always
+    recompute the scores in dq and ignore it."""
+    return dtype != torch.float32 and head_dim <= 128
+
+
 def _use_ds_workspace(nbytes: int, head_dim: int, ds) -> bool:
     """Whether the backward keeps dS' in a workspace of ``nbytes`` bytes
     (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy: on
@@ -192,9 +200,8 @@ class BackwardLaunch:
         self.dn = torch.empty((), device=dev, dtype=torch.float32)
         self.db = torch.empty((), device=dev, dtype=torch.float32)
         ds_bytes = int(self.lib.ssa_bwd_ds_workspace_bytes(B, Hq, N, int(bool(causal))))
-        # fp32 has no dS' workspace path (its dq always recomputes)
         self.ds = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-                   if q.dtype != torch.float32 and _use_ds_workspace(ds_bytes, D, ds) else None)
+                   if _has_ds_path(q.dtype, D) and _use_ds_workspace(ds_bytes, D, ds) else None)
         self.device = dev
         self.args = _lib.BwdArgs(
             _t4(self.q), _t4(self.k), _t4(self.v), _t4(self.out), _t4(self.dout),
@@ -367,7 +374,7 @@ def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen
     db = torch.empty((), device=dev, dtype=torch.float32)
     ds_bytes = int(lib.ssa_varlen_bwd_ds_workspace_bytes(docs, Hq, max_seqlen, T, int(bool(causal))))
     ds_ws = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-             if ds_bytes > 0 and q.dtype != torch.float32 and _use_ds_workspace(ds_bytes, D, ds) else None)
+             if ds_bytes > 0 and _has_ds_path(q.dtype, D) and _use_ds_workspace(ds_bytes, D, ds) else None)
     dense = _lib.BwdArgs(
         _t3(q), _t3(k), _t3(v), _t3(out), _t3(dout), _t3(dq), _t3(dk), _t3(dv),
         m.data_ptr(), delta.data_ptr(), partials.data_ptr(), dn.data_ptr(), db.data_ptr(),

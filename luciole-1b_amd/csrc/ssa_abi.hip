@@ -56,7 +56,7 @@ int32_t check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t N, int32_t D, i
   if (!shape_ok(B, Hq, Hkv, N)) return SSA_ERR_SHAPE;
   if (!packed && !rows_ok(B, Hq, N)) return SSA_ERR_SHAPE;
   if (dtype != SSA_DTYPE_BF16 && dtype != SSA_DTYPE_FP16 && dtype != SSA_DTYPE_FP32) return SSA_ERR_DTYPE;
-  if (D != 32 && D != 64 && D != 128 && !(D == 16 && dtype == SSA_DTYPE_FP32)) return SSA_ERR_HEAD_DIM;
+  if (D != 32 && D != 64 && D != 128 && D != 256 && !(D == 16 && dtype == SSA_DTYPE_FP32)) return SSA_ERR_HEAD_DIM;
   return SSA_OK;
 }
 
@@ -174,12 +174,12 @@ int32_t fill_bwd_params(const ssa_bwd_args* a, BwdParams* p, bool preprocess_onl
   return SSA_OK;
 }
 
-// dQ then the dn / db reduction: on the workspace path (bf16 / fp16 with a
-// dS' workspace) the dQ pass's first workgroup does the reduction, so it
-// needs no launch of its own.
+// dQ then the dn / db reduction: on the workspace path (the matrix-core
+// kernels with a dS' workspace) the dQ pass's first workgroup does the
+// reduction, so it needs no launch of its own.
 int32_t run_dq_and_reduce(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s) {
   BwdParams pq = p;
-  pq.fuse_reduce = p.ds != nullptr && dtype != SSA_DTYPE_FP32;
+  pq.fuse_reduce = p.ds != nullptr && !use_f32(dtype, D);
   SSA_TRY(launch_status(launch_bwd_dq(pq, dtype, D, causal, s)));
   return pq.fuse_reduce ? SSA_OK : launch_status(launch_reduce_partials(p, s));
 }
@@ -205,7 +205,7 @@ const char* ssa_status_string(int32_t status) {
       return "invalid shape (batch, heads, seqlen must be > 0 and Hq % Hkv == 0; size limits: seqlen and decode "
              "capacity <= 2^30, batch * heads_q * ceil(seqlen / 128) <= 2^28, at most 2^31 - 1 query rows per "
              "launch: batch * heads_q * seqlen, or heads_q * total_tokens for packed sequences)";
-    case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128; fp32 also 16)";
+    case SSA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128, 256; fp32 also 16)";
     case SSA_ERR_DTYPE: return "unsupported dtype (supported: bf16, fp16, fp32; the decode step bf16, fp16)";
     case SSA_ERR_ALIGNMENT:
       return "unsupported tensor layout (base pointer 16-byte aligned, strides non-negative multiples of 8 "

@@ -743,7 +743,7 @@ static hipError_t pre_dt(const BwdParams& p, int D, hipStream_t s) {
 }
 
 hipError_t launch_bwd_preprocess(const BwdParams& p, int dtype, int D, hipStream_t s) {
-  if (dtype == kDtypeF32) return launch_bwd_preprocess_f32(p, D, s);
+  if (use_f32(dtype, D)) return launch_bwd_preprocess_f32(p, dtype, D, s);
   return dtype == 0 ? pre_dt<__bf16>(p, D, s) : pre_dt<_Float16>(p, D, s);
 }
 
@@ -800,7 +800,7 @@ static hipError_t dq_t(const BwdParams& p, hipStream_t s) {
   }
 
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s) {
-  if (dtype == kDtypeF32) return launch_bwd_dkdv_f32(p, D, causal, s);
+  if (use_f32(dtype, D)) return launch_bwd_dkdv_f32(p, dtype, D, causal, s);
   if (dtype == 0) {
     SSA_DISPATCH(dkdv_t, __bf16, D, causal, p, s)
   }
@@ -808,7 +808,7 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, bool causal, hi
 }
 
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, bool causal, hipStream_t s) {
-  if (dtype == kDtypeF32) return launch_bwd_dq_f32(p, D, causal, s);
+  if (use_f32(dtype, D)) return launch_bwd_dq_f32(p, dtype, D, causal, s);
   if (dtype == 0) {
     SSA_DISPATCH(dq_t, __bf16, D, causal, p, s)
   }

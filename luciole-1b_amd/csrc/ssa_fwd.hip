@@ -458,7 +458,7 @@ static hipError_t launch_fwd_dt(const FwdParams& p, int D, bool causal, hipStrea
 }
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, bool causal, hipStream_t stream) {
-  if (dtype == kDtypeF32) return launch_fwd_f32(p, D, causal, stream);
+  if (use_f32(dtype, D)) return launch_fwd_f32(p, dtype, D, causal, stream);
   if (dtype == 0) return launch_fwd_dt<__bf16>(p, D, causal, stream);
   return launch_fwd_dt<_Float16>(p, D, causal, stream);
 }

@@ -7,8 +7,8 @@
 
 namespace ssa {
 
-// dtype: 0 = bf16, 1 = fp16 (D in {32, 64, 128}), 2 = fp32 (D in {16, 32, 64,
-// 128}, the vector-ALU kernels of ssa_f32.hip); validated by the caller.
+// dtype: 0 = bf16, 1 = fp16 (D in {32, 64, 128, 256}), 2 = fp32 (D in {16,
+// 32, 64, 128, 256}); validated by the caller.  Which kernels run: use_f32().
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
 hipError_t launch_bwd_preprocess(const BwdParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
@@ -21,12 +21,16 @@ hipError_t launch_reduce_partials(const BwdParams& p, hipStream_t stream);
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t stream);
 
-// fp32 inputs (ssa_f32.hip); the dS' workspace is not used (dQ recomputes).
+// The fp32-arithmetic vector-ALU kernels (ssa_f32.hip) run fp32 inputs at
+// every head dim and bf16 / fp16 inputs at head dim 256; the matrix-core
+// kernels run bf16 / fp16 at 32, 64 and 128.  The vector-ALU backward does
+// not use the dS' workspace (its dQ recomputes).
 constexpr int kDtypeF32 = 2;
-hipError_t launch_fwd_f32(const FwdParams& p, int D, bool causal, hipStream_t stream);
-hipError_t launch_bwd_preprocess_f32(const BwdParams& p, int D, hipStream_t stream);
-hipError_t launch_bwd_dkdv_f32(const BwdParams& p, int D, bool causal, hipStream_t stream);
-hipError_t launch_bwd_dq_f32(const BwdParams& p, int D, bool causal, hipStream_t stream);
+inline bool use_f32(int dtype, int D) { return dtype == kDtypeF32 || D == 256; }
+hipError_t launch_fwd_f32(const FwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
+hipError_t launch_bwd_preprocess_f32(const BwdParams& p, int dtype, int D, hipStream_t stream);
+hipError_t launch_bwd_dkdv_f32(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
+hipError_t launch_bwd_dq_f32(const BwdParams& p, int dtype, int D, bool causal, hipStream_t stream);
 
 }  // namespace ssa
 

@@ -138,7 +138,7 @@ def _bwd_args(**kw):
         ("batch", 0, _lib.SSA_ERR_SHAPE),
         ("seqlen", 0, _lib.SSA_ERR_SHAPE),
         ("head_dim", 96, _lib.SSA_ERR_HEAD_DIM),
-        ("head_dim", 256, _lib.SSA_ERR_HEAD_DIM),
+        ("head_dim", 512, _lib.SSA_ERR_HEAD_DIM),   # the largest is 256
         ("head_dim", 16, _lib.SSA_ERR_HEAD_DIM),    # bf16: D = 16 runs padded in Python, not here
         ("dtype", 7, _lib.SSA_ERR_DTYPE),
         ("m", None, _lib.SSA_ERR_NULL_POINTER),
@@ -156,8 +156,8 @@ def test_fwd_validation(field, value, status):
 
 
 def test_fp32_head_dims():
-    """fp32 takes head dims 16..128 (powers of two); other head dims stay refused."""
-    for D in (48, 96, 256, 8):
+    """fp32 takes head dims 16..256 (powers of two); other head dims stay refused."""
+    for D in (48, 96, 512, 8):
         a = _fwd_args(dtype=_lib.SSA_DTYPE_FP32, head_dim=D)
         assert _lib.lib().ssa_fwd(ctypes.byref(a), None) == _lib.SSA_ERR_HEAD_DIM, D
         b = _bwd_args(dtype=_lib.SSA_DTYPE_FP32, head_dim=D)

@@ -5,7 +5,7 @@ every output to match with atol 0 (determinism_atol=0.0), for each kernel
 dtype, N in {128, 1024}, causal and not, contiguous and strided inputs
 (training/train/train_ssa_triton/check_ssa_triton_parity.py:505-624, defaults
 :1021-1034).  Here: bf16, fp16 and fp32 inputs, head dims 32 (the reference's
-default) and 128 (the benchmark's), both backward paths of the 16-bit kernels
+default) and 128 (the benchmark's), 256 (the largest), both backward paths of the 16-bit kernels
 (dQ from the dS' workspace and dQ recomputed), GQA, and a packed stream.
 Every reduction in these kernels has a fixed order (no float atomics), so two
 runs agree bit for bit, dn and db included.
@@ -60,6 +60,26 @@ def test_two_runs_bitwise_equal(gpu, dtype, dq_path, N, causal, layout, D):
     def run():
         out, m = ssa_flash_attn_forward(q, k, v, scale, n, b, causal=causal)
         return (out, m) + tuple(ssa_flash_attn_backward(q, k, v, out, do, m, scale, n, b, causal=causal, ds=ds))
+
+    a, c = _twice(run)
+    _assert_same(label, ("out", "m", "dq", "dk", "dv", "dn", "db"), a, c)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_head_dim_256_bitwise_equal(gpu, dtype, causal):
+    """Head dim 256 runs on the vector-ALU kernels: the same fixed-order reductions."""
+    from SSA.ssa_triton_kernel import ssa_flash_attn_backward, ssa_flash_attn_forward
+
+    label = f"determinism {dtype} N=300 D=256 causal={int(causal)}"
+    print(f"[gpu case] {label}", file=sys.stderr, flush=True)
+    q, k, v, do = make_inputs(2, 4, 2, 300, 256, DTYPES[dtype], gpu, "contig", seed=4321)
+    n = torch.tensor(1.5, device=gpu)
+    b = torch.tensor(0.8, device=gpu)
+
+    def run():
+        out, m = ssa_flash_attn_forward(q, k, v, 1.0 / 16, n, b, causal=causal)
+        return (out, m) + tuple(ssa_flash_attn_backward(q, k, v, out, do, m, 1.0 / 16, n, b, causal=causal))
 
     a, c = _twice(run)
     _assert_same(label, ("out", "m", "dq", "dk", "dv", "dn", "db"), a, c)

@@ -101,7 +101,29 @@ def test_parity_fp32_trained_n(gpu):
     _check(*_run(gpu, 1, 4, 4, 300, 128, torch.float32, False, n_val=4.0, qkv_scale=0.5))
 
 
-@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("heads", [(4, 4), (8, 2)])
+@pytest.mark.parametrize("N", [7, 200])
+def test_parity_head_dim_256(gpu, dtype, causal, heads, N):
+    """Head dim 256 (the largest power of two the reference's Triton tiles take) on the
+    fp32-arithmetic vector-ALU kernels: bf16 / fp16 elements widened on load.  N = 200
+    fills the first 64-key pass of a 128-key block and part of the second."""
+    _check(*_run(gpu, 1, heads[0], heads[1], N, 256, dtype, causal))
+
+
+@pytest.mark.parametrize("layout", ["contig", "strided"])
+@pytest.mark.parametrize("N", [1, 129, 300])
+def test_parity_head_dim_256_ragged_strided(gpu, layout, N):
+    """Batch 2, GQA, Megatron-strided inputs; a dS' workspace asked for is ignored there."""
+    _check(*_run(gpu, 2, 4, 2, N, 256, torch.bfloat16, True, layout=layout, ds=True))
+
+
+def test_parity_head_dim_256_trained_n(gpu):
+    _check(*_run(gpu, 1, 4, 4, 300, 256, torch.float16, False, n_val=-3.484375, qkv_scale=0.5))
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("layout", ["contig", "strided"])
 def test_delta_direct(gpu, D, dtype, layout):
@@ -120,7 +142,7 @@ def test_delta_direct(gpu, D, dtype, layout):
     assert delta.shape == (2, 3, 300) and bool((err <= 1e-5 * mag + 1e-7).all()), float((err / (mag + 1e-12)).max())
 
 
-@pytest.mark.parametrize("D", [8, 256])
+@pytest.mark.parametrize("D", [8, 512])
 def test_unsupported_head_dims_raise(gpu, D):
     from SSA.ssa_triton_kernel import ssa_flash_attn_forward
 

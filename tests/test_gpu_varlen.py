@@ -79,6 +79,7 @@ CASES = [
     ((129, 31, 200), 4, 2, 128, False),
     ((40, 90, 257), 2, 2, 32, True),
     ((40, 90, 257), 4, 2, 16, True),  # head dim 16: zero-padded onto the D = 32 kernels
+    ((70, 3, 200), 4, 2, 256, True),  # head dim 256: the vector-ALU kernels (the dS' workspace unused)
 ]
 
 
@@ -164,7 +165,7 @@ def test_varlen_malformed_table_is_clamped(gpu, ds):
 
 
 @pytest.mark.parametrize("lens,D,causal", [((5, 100, 33, 260, 1), 128, True), ((40, 90, 257), 16, False),
-                                           ((7, 1, 33), 64, True)])
+                                           ((7, 1, 33), 64, True), ((70, 3, 200), 256, True)])
 def test_varlen_fp32(gpu, lens, D, causal):
     """fp32 token streams on the fp32 kernels, at the reference's fp32 tolerances."""
     label = f"varlen fp32 lens={lens} D={D} causal={int(causal)}"
