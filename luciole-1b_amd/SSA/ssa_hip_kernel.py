@@ -148,11 +148,26 @@ def _has_ds_path(dtype: torch.dtype, head_dim: int) -> bool:
     return dtype != torch.float32 and head_dim <= 128
 
 
-def _use_ds_workspace(nbytes: int, head_dim: int, ds) -> bool:
+def _device_headroom(device) -> int | None:
+    """Bytes a new allocation on ``device`` can take without the caching
+    allocator asking the driver for more than it has: the driver's free memory
+    plus what the allocator holds reserved but unused.  None if unknown."""
+    try:
+        free, _ = torch.cuda.mem_get_info(device)
+        return int(free) + int(torch.cuda.memory_reserved(device)) - int(torch.cuda.memory_allocated(device))
+    except (RuntimeError, AssertionError):
+        return None
+
+
+def _use_ds_workspace(nbytes: int, head_dim: int, ds, device=None) -> bool:
     """Whether the backward keeps dS' in a workspace of ``nbytes`` bytes
     (``ds``: True / False to force, None for the ``SSA_BWD_DS`` policy: on
-    within ``SSA_BWD_DS_MAX_BYTES``).  ``head_dim`` is kept for callers; every
-    head dim measured faster with the workspace."""
+    within ``SSA_BWD_DS_MAX_BYTES`` and, given ``device``, within half of its
+    headroom, so that the transient workspace (a per-layer spike of 2 bytes per
+    causal pair and head: 1.1 GB at B = 4, H = 16, S = 4096) never takes the
+    memory a training step needs; above either bound dq recomputes the scores
+    instead).  ``head_dim`` is kept for callers; every head dim measured faster
+    with the workspace."""
     if ds is not None:
         return bool(ds)
     mode = os.environ.get("SSA_BWD_DS", "auto").strip().lower()
@@ -161,7 +176,10 @@ def _use_ds_workspace(nbytes: int, head_dim: int, ds) -> bool:
     if mode in ("1", "on", "true", "yes"):
         return True
     limit = int(os.environ.get("SSA_BWD_DS_MAX_BYTES", str(16 << 30)))
-    return 0 < nbytes <= limit
+    if not 0 < nbytes <= limit:
+        return False
+    room = _device_headroom(device) if device is not None else None
+    return room is None or nbytes <= room // 2
 
 
 class BackwardLaunch:
@@ -201,7 +219,7 @@ class BackwardLaunch:
         self.db = torch.empty((), device=dev, dtype=torch.float32)
         ds_bytes = int(self.lib.ssa_bwd_ds_workspace_bytes(B, Hq, N, int(bool(causal))))
         self.ds = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-                   if _has_ds_path(q.dtype, D) and _use_ds_workspace(ds_bytes, D, ds) else None)
+                   if _has_ds_path(q.dtype, D) and _use_ds_workspace(ds_bytes, D, ds, dev) else None)
         self.device = dev
         self.args = _lib.BwdArgs(
             _t4(self.q), _t4(self.k), _t4(self.v), _t4(self.out), _t4(self.dout),
@@ -374,7 +392,7 @@ def ssa_flash_attn_varlen_backward(q, k, v, out, dout, m, cu_seqlens, max_seqlen
     db = torch.empty((), device=dev, dtype=torch.float32)
     ds_bytes = int(lib.ssa_varlen_bwd_ds_workspace_bytes(docs, Hq, max_seqlen, T, int(bool(causal))))
     ds_ws = (torch.empty(ds_bytes, device=dev, dtype=torch.uint8)
-             if ds_bytes > 0 and _has_ds_path(q.dtype, D) and _use_ds_workspace(ds_bytes, D, ds) else None)
+             if ds_bytes > 0 and _has_ds_path(q.dtype, D) and _use_ds_workspace(ds_bytes, D, ds, dev) else None)
     dense = _lib.BwdArgs(
         _t3(q), _t3(k), _t3(v), _t3(out), _t3(dout), _t3(dq), _t3(dk), _t3(dv),
         m.data_ptr(), delta.data_ptr(), partials.data_ptr(), dn.data_ptr(), db.data_ptr(),

@@ -595,3 +595,35 @@ def test_ds_workspace_policy(monkeypatch):
     assert not _use_ds_workspace(1 << 10, 128, None)
     monkeypatch.setenv("SSA_BWD_DS", "1")
     assert _use_ds_workspace(1 << 40, 32, None)
+
+
+def test_ds_workspace_policy_leaves_headroom(monkeypatch):
+    """Given a device, the automatic policy also keeps the workspace within half
+    of the device's headroom (driver-free plus allocator-cached memory), so a
+    large transient dS' never crowds out a training step: above it dq
+    recomputes.  Forcing (SSA_BWD_DS=1 or ds=True) overrides it."""
+    import SSA.ssa_hip_kernel as hk
+
+    monkeypatch.delenv("SSA_BWD_DS", raising=False)
+    monkeypatch.delenv("SSA_BWD_DS_MAX_BYTES", raising=False)
+    monkeypatch.setattr(hk, "_device_headroom", lambda device: 8 << 30)
+    assert hk._use_ds_workspace(4 << 30, 128, None, "cuda:0")
+    assert not hk._use_ds_workspace((4 << 30) + 1, 128, None, "cuda:0")
+    assert hk._use_ds_workspace(6 << 30, 128, True, "cuda:0")
+    assert hk._use_ds_workspace(6 << 30, 128, None)          # no device: the byte cap alone
+    monkeypatch.setattr(hk, "_device_headroom", lambda device: None)  # unknown: the cap alone
+    assert hk._use_ds_workspace(6 << 30, 128, None, "cuda:0")
+    monkeypatch.setenv("SSA_BWD_DS", "1")
+    monkeypatch.setattr(hk, "_device_headroom", lambda device: 0)
+    assert hk._use_ds_workspace(6 << 30, 128, None, "cuda:0")
+
+
+def test_ds_path_by_dtype_and_head_dim():
+    """Only the matrix-core kernels (bf16 / fp16, head dims up to 128) use a dS'
+    workspace; fp32 and head dim 256 run the vector-ALU kernels, whose dq recomputes."""
+    import torch
+
+    from SSA.ssa_hip_kernel import _has_ds_path
+
+    assert _has_ds_path(torch.bfloat16, 128) and _has_ds_path(torch.float16, 32)
+    assert not _has_ds_path(torch.bfloat16, 256) and not _has_ds_path(torch.float32, 64)
