@@ -20,7 +20,9 @@ buffer stores of csrc/ssa_tile.hpp) is not protected against:
 With fewer, the memory instruction can read the register's previous value
 and so access a wrong address (or, for the store data, store the new value).  ``scan_asm`` walks a device .s file in
 program order (a label does not reset the window, so fall-through paths are
-covered) and returns every site with fewer wait states than required.
+covered; an unconditional transfer -- s_endpgm, s_branch, s_setpc -- does,
+since the instruction after it is never its successor) and returns every
+site with fewer wait states than required.
 
 The dK/dV accumulators are MFMAs issued from inline assembly into AGPRs
 (mfma32_acc / acc_fence in csrc/ssa_common.hpp), which the compiler's hazard
@@ -133,6 +135,8 @@ def scan_asm(text: str) -> list:
             if WIDE_STORE.match(parts[0]) and len(parts) > 2:
                 data = _vregs(parts[1] if parts[0].startswith("buffer_") else parts[2])
             window.append((_valu_sgpr_defs(parts), _salu_m0_def(parts), data))
+            if parts[0] in ("s_endpgm", "s_branch", "s_setpc_b64"):
+                window = []
         del window[:-8]
     return sites
 

@@ -477,6 +477,11 @@ def test_hazard_scan_flags_store_data_overwrite():
     b = "buffer_store_dwordx4 v[20:23], v2, s[8:11], s4 offen offset:512 nt"
     assert sites([b, "s_nop 0", "v_add_u32_e32 v21, 1, v21"]) == [(1, 2)]
     assert sites(["global_store_dwordx2 v[10:11], v[4:5], off", "v_mov_b32_e32 v4, 0"]) == []
+    # the instruction after an unconditional transfer is not the store's successor,
+    # while a plain label (a fall-through) still is
+    assert sites([g, ".LBB0_7:", "s_endpgm", ".LBB0_8:", "v_add_u32_e32 v4, s26, v105"]) == []
+    assert sites([g, "s_branch .LBB0_9", ".LBB0_8:", "v_add_u32_e32 v4, s26, v105"]) == []
+    assert sites([g, ".LBB0_8:", "v_add_u32_e32 v4, s26, v105"]) == [(0, 2)]
 
 
 def test_agpr_scan_follows_every_path():
