@@ -1,9 +1,10 @@
 """ssa_bwd_noalloc: the backward that allocates nothing (Delta and the dn/db
 partials in the library's static device scratch, dQ recomputed).
 
-Called through the C ABI on three problems in a row -- each smaller, so each
-runs on the scratch the previous one left behind, the last on the fp32
-kernels -- and compared with ssa_bwd on
+Called through the C ABI on four problems in a row -- each smaller, so each
+runs on the scratch the previous one left behind, the last two on the
+vector-ALU kernels (fp32 at head dim 16, bf16 at head dim 256) -- and
+compared with ssa_bwd on
 the same arguments (recompute path, caller workspaces): bitwise equal, and
 within the parity bar of the fp64 oracle (tests/parity_util.py).  The
 caller's delta / partials fields are NULL, so nothing of the caller's is used
@@ -24,15 +25,16 @@ from parity_util import assert_parity, compare, make_inputs, oracle_fwd_bwd, sca
 pytestmark = pytest.mark.gpu
 
 CALLS = [
-    # B, Hq, Hkv, N, D, causal, dtype: larger first, then smaller (the last on
-    # the fp32 kernels, to the fp32 bars)
+    # B, Hq, Hkv, N, D, causal, dtype: larger first, then smaller (the last two
+    # on the vector-ALU kernels: fp32 to the fp32 bars, bf16 at head dim 256)
     (2, 8, 4, 700, 128, True, torch.bfloat16),
     (1, 4, 2, 200, 64, False, torch.bfloat16),
     (1, 4, 4, 150, 16, True, torch.float32),
+    (1, 2, 2, 130, 256, True, torch.bfloat16),
 ]
 
 
-def test_noalloc_equals_ssa_bwd_on_three_calls(gpu):
+def test_noalloc_equals_ssa_bwd_on_four_calls(gpu):
     from SSA import _lib
     from SSA.ssa_hip_kernel import BackwardLaunch, ssa_flash_attn_forward
 
