@@ -27,13 +27,16 @@ a transient workspace so that dQ is one streaming product with K instead of
 the reference's recompute of the scores (measured faster at every head dim:
 3-6 % of the backward at D = 32 / 64, 7-17 % at D = 128); ``SSA_BWD_DS=0`` /
 ``1`` forces either path, and a workspace above ``SSA_BWD_DS_MAX_BYTES``
-(default 16 GiB) always recomputes.  Head dims 32, 64 and 128 run on kernels of their own; in bf16 /
+(default 16 GiB) or half of the device's headroom recomputes.  Head dims 32,
+64 and 128 run on kernels of their own; in bf16 /
 fp16, head dim 16 (the smallest the reference's Triton kernel takes) runs on
 the D = 32 kernels with its operands zero-padded to 32 columns, which changes
 no score, dP or Delta, and the results are sliced back (the decode step is not
 offered at D = 16).  fp32 inputs (the reference's fp32-operand path) run on
-fp32 vector-ALU kernels for head dims 16-128 that keep every product in fp32,
-without the dS' workspace; the decode step takes bf16 / fp16 only.  Errors:
+fp32 vector-ALU kernels for head dims 16-256 that keep every product in fp32,
+without the dS' workspace; bf16 / fp16 at head dim 256 (the largest power of
+two the reference takes) run on the same kernels, widened on load (coverage,
+not speed); the decode step takes bf16 / fp16 only.  Errors:
 ``AssertionError`` for ``Hq % Hkv != 0`` and a non-power-of-two head dim, as in
 the reference; ``ValueError`` for other head dims and other dtypes.
 """
